@@ -1,0 +1,444 @@
+/*
+ * lal_oracle.c -- CPU restatement of LAL's token-sampling path.
+ *
+ * TEST INFRASTRUCTURE ONLY (the parity checker).  It is never linked into the
+ * product library; only tests/, the smoke check and bench.py's cpu_baseline
+ * leg load it.  Reference anchors are given per function; the full list is in
+ * lal_oracle.h.
+ */
+#include "lal_oracle.h"
+
+#include <math.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+float lal_oracle_expf(float x) { return expf(x); }
+
+/* ---------------------------------------------------------------------------
+ * k-th largest with multiplicity, by a size-k min-heap whose root is replaced
+ * only by a strictly larger value (runtime/lal_sampling.h:69-104,
+ * tools/server/qwen7b_server.c:237-256).
+ * ------------------------------------------------------------------------- */
+static float heap_kth_largest(const float *y, int n, int k, float *heap)
+{
+    int size = 0;
+    heap[0] = -INFINITY;
+    for (int v = 0; v < n; v++) {
+        float val = y[v];
+        if (size < k) {
+            int c = size++;
+            heap[c] = val;
+            while (c > 0) {
+                int up = (c - 1) >> 1;
+                if (heap[up] <= heap[c]) break;
+                float t = heap[up]; heap[up] = heap[c]; heap[c] = t;
+                c = up;
+            }
+        } else if (val > heap[0]) {
+            heap[0] = val;
+            int at = 0;
+            for (;;) {
+                int a = 2 * at + 1, b = a + 1, lo = at;
+                if (a < size && heap[a] < heap[lo]) lo = a;
+                if (b < size && heap[b] < heap[lo]) lo = b;
+                if (lo == at) break;
+                float t = heap[at]; heap[at] = heap[lo]; heap[lo] = t;
+                at = lo;
+            }
+        }
+    }
+    return heap[0];
+}
+
+static int cmp_desc(const void *a, const void *b)
+{
+    float x = *(const float *)a, y = *(const float *)b;
+    return (x < y) - (x > y);
+}
+
+float lal_oracle_kth_largest_sorted(const float *x, int n, int k)
+{
+    float *tmp = (float *)malloc((size_t)n * sizeof(float));
+    memcpy(tmp, x, (size_t)n * sizeof(float));
+    qsort(tmp, (size_t)n, sizeof(float), cmp_desc);
+    float r = tmp[k - 1];
+    free(tmp);
+    return r;
+}
+
+/* Stable descending sort of (prob, id) pairs: equal probabilities keep their
+ * input (ascending-id) order, which is what the insertion sort of
+ * gpt2_server.c:2934-2945 produces.  Bottom-up merge sort so that large tie
+ * groups stay O(n log n). */
+static void stable_sort_desc(float *p, int *id, int n, float *tp, int *tid)
+{
+    for (int w = 1; w < n; w *= 2) {
+        for (int lo = 0; lo < n; lo += 2 * w) {
+            int mid = lo + w < n ? lo + w : n;
+            int hi = lo + 2 * w < n ? lo + 2 * w : n;
+            int i = lo, j = mid, o = lo;
+            while (i < mid && j < hi) {
+                /* take from the right only when strictly larger */
+                if (p[j] > p[i]) { tp[o] = p[j]; tid[o++] = id[j++]; }
+                else             { tp[o] = p[i]; tid[o++] = id[i++]; }
+            }
+            while (i < mid) { tp[o] = p[i]; tid[o++] = id[i++]; }
+            while (j < hi)  { tp[o] = p[j]; tid[o++] = id[j++]; }
+        }
+        memcpy(p, tp, (size_t)n * sizeof(float));
+        memcpy(id, tid, (size_t)n * sizeof(int));
+    }
+}
+
+static void apply_penalty(float *row, int V, float pen, const int *hist, int n_hist)
+{
+    /* lal_sampling.h:59-67: once per history occurrence, in order */
+    if (!(pen > 1.0f) || !hist || n_hist <= 0) return;
+    for (int i = 0; i < n_hist; i++) {
+        int t = hist[i];
+        if (t < 0 || t >= V) continue;
+        if (row[t] > 0) row[t] = row[t] / pen;
+        else            row[t] = row[t] * pen;
+    }
+}
+
+static int argmax_first(const float *y, int V)
+{
+    int best = 0;
+    for (int v = 1; v < V; v++)
+        if (y[v] > y[best]) best = v;
+    return best;
+}
+
+int lal_oracle_sample_row(float *row, int V, const lal_oracle_params *p,
+                          const int *hist, int n_hist,
+                          const uint32_t *allow, const float *bias, float u,
+                          lal_oracle_filter_fn filter, lal_oracle_decode_fn decode,
+                          lal_oracle_info *info,
+                          int cand_cap, int *cand_ids, float *cand_probs,
+                          unsigned char *cand_kept)
+{
+    lal_oracle_info inf;
+    memset(&inf, 0, sizeof inf);
+    const float T = p->temperature;
+    const int greedy = (T <= 0.0f || p->top_k <= 0);
+    int token = V - 1;
+
+    if (p->variant == LAL_ORACLE_VARIANT_FILTERED)
+        apply_penalty(row, V, p->rep_penalty, hist, n_hist);
+    else if (!greedy)
+        apply_penalty(row, V, p->rep_penalty, hist, n_hist);
+
+    /* processed logits: bias -> allow bitmask -> hard anti-repeat */
+    float *y = (float *)malloc((size_t)V * sizeof(float));
+    for (int v = 0; v < V; v++) {
+        float x = row[v];
+        if (bias) x = x + bias[v];
+        if (allow && !((allow[v >> 5] >> (v & 31)) & 1u)) x = -INFINITY;
+        y[v] = x;
+    }
+    if (p->mask_recent > 0 && hist) {
+        int s = n_hist > p->mask_recent ? n_hist - p->mask_recent : 0;
+        for (int i = s; i < n_hist; i++) {
+            int t = hist[i];
+            if (t >= 0 && t < V) y[t] = -INFINITY;
+        }
+    }
+
+    if (greedy) {
+        token = argmax_first(y, V);
+        inf.greedy = 1;
+        inf.threshold = y[token];
+        int n = 0;
+        for (int v = 0; v < V; v++) n += (y[v] >= inf.threshold);
+        inf.n_cand = n;
+        inf.n_kept = 1;
+        if (info) *info = inf;
+        free(y);
+        return token;
+    }
+
+    int k = p->top_k;
+    if (k > V) k = V;
+    if (k < 1) k = 1;
+    float *heap = (float *)malloc((size_t)k * sizeof(float));
+    const float thr = heap_kth_largest(y, V, k, heap);
+    free(heap);
+
+    int *cand = (int *)malloc((size_t)V * sizeof(int));
+    int *keep = (int *)malloc((size_t)V * sizeof(int));
+    int n_cand = 0;
+    for (int v = 0; v < V; v++) {
+        int c = (y[v] >= thr);
+        if (c) cand[n_cand++] = v;
+        keep[v] = c;
+    }
+
+    /* top-p nucleus over the top-k pool (gpt2_server.c:2908-2955) */
+    if (p->top_p > 0.0f && p->top_p < 1.0f && n_cand > 0) {
+        float *pr = (float *)malloc((size_t)n_cand * sizeof(float));
+        int *id = (int *)malloc((size_t)n_cand * sizeof(int));
+        float *tp = (float *)malloc((size_t)n_cand * sizeof(float));
+        int *tid = (int *)malloc((size_t)n_cand * sizeof(int));
+        float amax = -1e30f;
+        for (int i = 0; i < n_cand; i++)
+            if (y[cand[i]] > amax) amax = y[cand[i]];
+        float se = 0.0f;
+        for (int i = 0; i < n_cand; i++) {
+            pr[i] = expf((y[cand[i]] - amax) / T);
+            se += pr[i];
+            id[i] = cand[i];
+        }
+        float inv = 1.0f / (se + 1e-12f);
+        for (int i = 0; i < n_cand; i++) pr[i] *= inv;
+        stable_sort_desc(pr, id, n_cand, tp, tid);
+        for (int i = 0; i < n_cand; i++) keep[cand[i]] = 0;
+        float cum = 0.0f;
+        for (int i = 0; i < n_cand; i++) {
+            keep[id[i]] = 1;
+            cum += pr[i];
+            if (cum >= p->top_p) break;
+        }
+        free(pr); free(id); free(tp); free(tid);
+    }
+
+    /* lal.py filter ops on the keep mask (compiler/lal.py:2220-2242), then an
+     * optional plugin with the lal_filter_topk ABI, then restore-if-empty
+     * (qwen7b_server.c:260-269). */
+    {
+        int last = (n_hist > 0 && hist) ? hist[n_hist - 1] : -1;
+        if (p->ban_last && last >= 0 && last < V) keep[last] = 0;
+        if (p->ban_repeat > 0 && hist) {
+            int s = n_hist > p->ban_repeat ? n_hist - p->ban_repeat : 0;
+            for (int i = s; i < n_hist; i++) {
+                int t = hist[i];
+                if (t >= 0 && t < V) keep[t] = 0;
+            }
+        }
+        for (int i = 0; i < p->n_ban_ids; i++) {
+            int t = p->ban_ids[i];
+            if (t >= 0 && t < V) keep[t] = 0;
+        }
+        if (filter) filter(keep, V, last, hist, n_hist, decode);
+        int any = 0;
+        for (int i = 0; i < n_cand; i++) if (keep[cand[i]]) { any = 1; break; }
+        /* a plugin may only clear entries; anything it sets outside the pool
+         * is still honoured as the reference does (keep_mask is read as-is) */
+        if (!any) {
+            for (int v = 0; v < V; v++) if (keep[v]) { any = 1; break; }
+        }
+        if (!any)
+            for (int i = 0; i < n_cand; i++) keep[cand[i]] = 1;
+    }
+
+    /* softmax over the kept set, ascending id, sequential fp32 */
+    float mx = -1e30f;
+    for (int v = 0; v < V; v++)
+        if (keep[v] && y[v] >= thr && y[v] > mx) mx = y[v];
+    float sum = 0.0f;
+    int n_kept = 0;
+    for (int v = 0; v < V; v++)
+        if (keep[v] && y[v] >= thr) { sum += expf((y[v] - mx) / T); n_kept++; }
+
+    inf.threshold = thr;
+    inf.n_cand = n_cand;
+    inf.n_kept = n_kept;
+    inf.sum = sum;
+
+    if (p->variant == LAL_ORACLE_VARIANT_FILTERED && sum <= 0) {
+        /* qwen7b_server.c:285-286: argmax over the kept set, no draw */
+        int best = 0;
+        float bv = -1e30f;
+        for (int v = 0; v < V; v++)
+            if (keep[v] && y[v] > bv) { bv = y[v]; best = v; }
+        token = best;
+    } else {
+        inf.used_uniform = 1;
+        float r = u * sum;
+        token = V - 1;
+        if ((p->flags & LAL_ORACLE_F_DRAW_GPT2) && r == 0.0f) {
+            token = 0;
+        } else {
+            float acc = 0.0f;
+            for (int v = 0; v < V; v++) {
+                if (keep[v] && y[v] >= thr) {
+                    acc += expf((y[v] - mx) / T);
+                    if (r <= acc) { token = v; break; }
+                }
+            }
+        }
+    }
+
+    if (cand_ids || cand_probs || cand_kept) {
+        int m = n_cand < cand_cap ? n_cand : cand_cap;
+        for (int i = 0; i < m; i++) {
+            int v = cand[i];
+            int kp = keep[v] != 0;
+            if (cand_ids) cand_ids[i] = v;
+            if (cand_kept) cand_kept[i] = (unsigned char)kp;
+            if (cand_probs) cand_probs[i] = kp ? expf((y[v] - mx) / T) / sum : 0.0f;
+        }
+    }
+    free(cand); free(keep); free(y);
+    if (info) *info = inf;
+    return token;
+}
+
+void lal_oracle_sample_batch(float *logits, int B, int V, int ld,
+                             const lal_oracle_params *p,
+                             const int *hist, int hist_ld, const int *hist_len,
+                             const uint32_t *allow, int allow_ld,
+                             const float *bias, const float *uniforms,
+                             int *out_token, float *out_threshold,
+                             int *out_n_cand, int *out_n_kept, float *out_sum,
+                             int cand_ld, int *cand_ids, float *cand_probs,
+                             unsigned char *cand_kept, int nthreads)
+{
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int b = 0; b < B; b++) {
+        lal_oracle_info inf;
+        const int *h = hist ? hist + (size_t)b * hist_ld : NULL;
+        int nh = hist ? (hist_len ? hist_len[b] : hist_ld) : 0;
+        const uint32_t *al = allow ? allow + (size_t)b * allow_ld : NULL;
+        size_t co = (size_t)b * (cand_ld > 0 ? cand_ld : 0);
+        out_token[b] = lal_oracle_sample_row(
+            logits + (size_t)b * ld, V, p, h, nh, al, bias, uniforms[b],
+            NULL, NULL, &inf, cand_ld,
+            cand_ids ? cand_ids + co : NULL,
+            cand_probs ? cand_probs + co : NULL,
+            cand_kept ? cand_kept + co : NULL);
+        if (out_threshold) out_threshold[b] = inf.threshold;
+        if (out_n_cand) out_n_cand[b] = inf.n_cand;
+        if (out_n_kept) out_n_kept[b] = inf.n_kept;
+        if (out_sum) out_sum[b] = inf.sum;
+    }
+#ifndef _OPENMP
+    (void)nthreads;
+#endif
+}
+
+void lal_oracle_uniforms(unsigned seed, int n, float *out, int gpt2)
+{
+    srand(seed);
+    for (int i = 0; i < n; i++) {
+        if (gpt2) out[i] = (float)(rand() % 1000000) / 1000000.0f;
+        else      out[i] = (float)rand() / (float)RAND_MAX;
+    }
+}
+
+/* lal_q8_kernel.h:375-442.  The AVX2 build converts the multiple-of-8 prefix
+ * with round-to-nearest-even (cvtps_epi32 under the default MXCSR) and the
+ * remainder with C truncation; the scalar build truncates everything. */
+float lal_oracle_quantize_x(const float *x, int8_t *xq, int n, int mode)
+{
+    float m = 0.0f;
+    for (int i = 0; i < n; i++) {
+        float a = fabsf(x[i]);
+        if (a > m) m = a;
+    }
+    float scale = m / 127.0f;
+    if (scale < 1e-8f) scale = 1e-8f;
+    float inv = 1.0f / scale;
+    int rne_end = (mode == 0) ? (n & ~7) : 0;
+    for (int i = 0; i < n; i++) {
+        float s = x[i] * inv;
+        int q = (i < rne_end) ? (int)nearbyintf(s) : (int)s;
+        if (q > 127) q = 127;
+        if (q < -127) q = -127;
+        xq[i] = (int8_t)q;
+    }
+    return scale;
+}
+
+/* lal_q8_kernel.h:463-499: exact int32 dot, then (sx*sw[v])*(float)dot */
+void lal_oracle_lm_head(float *logits, const int8_t *xq, float sx,
+                        const int8_t *W, const float *sw, int v0, int v1,
+                        int n, int nthreads)
+{
+#ifdef _OPENMP
+    if (nthreads <= 0) nthreads = omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthreads)
+#endif
+    for (int v = v0; v < v1; v++) {
+        const int8_t *w = W + (size_t)v * n;
+        int32_t dot = 0;
+        for (int i = 0; i < n; i++) dot += (int32_t)xq[i] * (int32_t)w[i];
+        logits[v] = sx * sw[v] * (float)dot;
+    }
+#ifndef _OPENMP
+    (void)nthreads;
+#endif
+}
+
+/* lal_q8_kernel.h:357-372: per-row absmax, lroundf (half away from zero) */
+void lal_oracle_quantize_w(const float *W, int8_t *q, float *scale,
+                           int in_dim, int out_dim)
+{
+    for (int j = 0; j < out_dim; j++) {
+        const float *r = W + (size_t)j * in_dim;
+        float m = 0.0f;
+        for (int i = 0; i < in_dim; i++) {
+            float a = fabsf(r[i]);
+            if (a > m) m = a;
+        }
+        float s = m / 127.0f;
+        if (s < 1e-8f) s = 1e-8f;
+        scale[j] = s;
+        float inv = 1.0f / s;
+        for (int i = 0; i < in_dim; i++) {
+            long t = lroundf(r[i] * inv);
+            if (t > 127) t = 127;
+            if (t < -127) t = -127;
+            q[(size_t)j * in_dim + i] = (int8_t)t;
+        }
+    }
+}
+
+/* Filter plugins with the lal_filter_topk ABI (compiler/lal.py:2205-2242):
+ * each ban clears a still-kept id and counts it.  antirepeat4 is what
+ * demos/mini_antirepeat.lal declares (ban_last; ban_repeat(4)); norepeat6 is
+ * the id rules of demos/qwen_filter.lal (ban_last; ban_repeat(6)). */
+static int ban_recent(int *keep, int V, int last, const int *rec, int n, int rep)
+{
+    int dropped = 0;
+    if (last >= 0 && last < V && keep[last]) { keep[last] = 0; dropped++; }
+    int s = n > rep ? n - rep : 0;
+    for (int i = s; i < n; i++) {
+        int t = rec[i];
+        if (t >= 0 && t < V && keep[t]) { keep[t] = 0; dropped++; }
+    }
+    return dropped;
+}
+
+int lal_oracle_filter_antirepeat4(int *keep_mask, int n_vocab, int last_token,
+                                  const int *recent, int n_recent,
+                                  lal_oracle_decode_fn decode_fn)
+{
+    (void)decode_fn;
+    return ban_recent(keep_mask, n_vocab, last_token, recent, n_recent, 4);
+}
+
+int lal_oracle_filter_norepeat6(int *keep_mask, int n_vocab, int last_token,
+                                const int *recent, int n_recent,
+                                lal_oracle_decode_fn decode_fn)
+{
+    (void)decode_fn;
+    return ban_recent(keep_mask, n_vocab, last_token, recent, n_recent, 6);
+}
+
+/* lal_sampling.h:133-136: append, or drop the oldest once 256 are held */
+void lal_oracle_recent_push(lal_oracle_recent *rt, int tok)
+{
+    if (rt->n < 256) {
+        rt->tokens[rt->n++] = tok;
+        return;
+    }
+    memmove(rt->tokens, rt->tokens + 1, 255 * sizeof(int));
+    rt->tokens[255] = tok;
+}
