@@ -1,0 +1,165 @@
+/*
+ * lal_gpu_sample.h -- C ABI of the MI355X (gfx950) token sampler.
+ *
+ * One shared library (liblal_gpu.so, built from lal_amd/csrc/lal_gpu_sample.hip)
+ * exports these plain-C entry points.  Pointers named d_* / marked "device"
+ * are HIP device pointers; streams are hipStream_t passed as void*.  Calls are
+ * asynchronous on the given stream unless stated otherwise and never exit():
+ * errors are returned as negative LAL_GPU_E_* codes.
+ *
+ * What each entry point replaces in samaidev/lal (the reference is CPU-only,
+ * header-only C; its interface is source-level):
+ *   lal_gpu_sample         runtime/lal_sampling.h:46-125   lal_sample_token
+ *                          tools/server/qwen7b_server.c:219-295
+ *                                                  lal_sample_token_filtered
+ *                          tools/server/gpt2_server.c:2862-3012 (top-p)
+ *                          compiler/lal.py:2218-2242 lal_filter_topk bans
+ *                          (ban_last / ban_repeat(n) / ban_token(id)) on the
+ *                          top-k pool, batched over rows
+ *   lal_gpu_quantize_x     runtime/lal_q8_kernel.h:375-442 lal_quantize_x_int8
+ *   lal_gpu_lm_head_q8     runtime/lal_q8_kernel.h:463-543
+ *                          lal_lm_head_int8_range[_abs], caller
+ *                          tools/server/qwen7b_server.c:829-845
+ *   lal_gpu_uniforms_rand  runtime/lal_sampling.h:116 ((float)rand()/RAND_MAX)
+ * The source-compatible drop-in for runtime/lal_sampling.h is
+ * include/lal_sampling.h, built on these entry points.
+ */
+#ifndef LAL_GPU_SAMPLE_H
+#define LAL_GPU_SAMPLE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define LAL_GPU_ABI_VERSION 1
+
+/* Limits.  top_k is capped at 512, the largest heap the reference samplers
+ * hold (tools/server/qwen7b_server.c:239); beyond it the reference is
+ * undefined behaviour. */
+#define LAL_GPU_MAX_K        512
+#define LAL_GPU_MAX_HISTORY  512   /* history ids per row (the reference ring holds 256) */
+#define LAL_GPU_MAX_BAN_IDS  64    /* ban_token ids per call */
+
+/* Return codes */
+#define LAL_GPU_OK        0
+#define LAL_GPU_E_INVAL  (-1)  /* null or inconsistent argument */
+#define LAL_GPU_E_RANGE  (-2)  /* size above a context or library limit */
+#define LAL_GPU_E_HIP    (-3)  /* HIP runtime error (see lal_gpu_last_hip_error) */
+#define LAL_GPU_E_NOMEM  (-4)
+#define LAL_GPU_E_NODEV  (-5)
+
+/* Sampler variants */
+#define LAL_GPU_VARIANT_BASIC    0 /* lal_sample_token: greedy test before the
+                                      penalty (lal_sampling.h:51-67) */
+#define LAL_GPU_VARIANT_FILTERED 1 /* lal_sample_token_filtered: penalty first,
+                                      sum<=0 -> argmax of the kept set without
+                                      a draw (qwen7b_server.c:223-286) */
+
+/* Flags */
+#define LAL_GPU_F_WRITEBACK  0x1u /* write the penalised value back into
+                                     logits[row][t] for every history id t, the
+                                     reference's in-place side effect */
+#define LAL_GPU_F_DRAW_GPT2  0x2u /* gpt2_server.c:2997-3002 draw: r == 0
+                                     returns token 0 */
+
+typedef struct lal_gpu_ctx lal_gpu_ctx;
+
+typedef struct lal_gpu_sample_params {
+    float temperature;  /* <= 0: greedy (first index of the maximum) */
+    int   top_k;        /* <= 0: greedy; clamped to vocab; <= LAL_GPU_MAX_K */
+    float top_p;        /* nucleus over the top-k pool when 0 < top_p < 1 */
+    float rep_penalty;  /* applied when > 1: x>0 ? x/p : x*p per occurrence */
+    int   variant;      /* LAL_GPU_VARIANT_* */
+    unsigned flags;     /* LAL_GPU_F_* */
+    /* lal_filter_topk ops on the top-k pool (post-selection, no refill; the
+     * pool is restored when they drop every token) */
+    int   ban_last;     /* 1: drop history[len-1] */
+    int   ban_repeat;   /* n > 0: drop history[max(0,len-n) .. len-1] */
+    int   n_ban_ids;    /* ban_token(id) list, device int[n_ban_ids] */
+    const int *ban_ids;
+    /* logit-space op before selection: the last n history ids become -inf */
+    int   mask_recent;
+} lal_gpu_sample_params;
+
+typedef struct lal_gpu_sample_io {
+    /* inputs (device) */
+    float          *logits;      /* [batch][ld] fp32; read-only unless WRITEBACK */
+    int             ld;          /* row stride in floats, >= vocab */
+    const int      *history;     /* [batch][history_ld] token ids, or NULL */
+    int             history_ld;
+    const int      *history_len; /* [batch] ids used per row, or NULL: history_ld */
+    const uint32_t *allow_bits;  /* [batch][allow_ld] words, token v allowed when
+                                    bit (v&31) of word (v>>5) is set; or NULL */
+    int             allow_ld;    /* >= ceil(vocab/32) */
+    const float    *bias;        /* [vocab] additive logit bias, or NULL */
+    const float    *uniforms;    /* [batch] one uniform in [0,1] per row */
+    /* outputs (device) */
+    int            *out_token;   /* [batch] sampled ids */
+    /* optional outputs (device, NULL to skip) */
+    float          *out_threshold; /* [batch] k-th largest processed logit */
+    int            *out_n_cand;    /* [batch] #processed logits >= threshold */
+    int            *out_n_kept;    /* [batch] #tokens in the final set */
+    float          *out_sum;       /* [batch] softmax denominator of the final set */
+    int             cand_ld;       /* per-row capacity of the candidate arrays */
+    int            *cand_ids;      /* [batch][cand_ld] pool ids, ascending */
+    float          *cand_probs;    /* [batch][cand_ld] e/sum if kept, else 0 */
+    uint8_t        *cand_kept;     /* [batch][cand_ld] 1 if in the final set */
+    float          *out_history_vals; /* [batch][history_ld] logits[t] after the
+                                         penalty for each history position */
+} lal_gpu_sample_io;
+
+/* Context: owns per-device scratch sized for max_batch x max_vocab.
+ * One context per host thread / stream. */
+int  lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab);
+void lal_gpu_destroy(lal_gpu_ctx *ctx);
+
+/* Batched sampler: one token per row. */
+int  lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab,
+                    const lal_gpu_sample_params *params,
+                    const lal_gpu_sample_io *io, void *stream);
+
+/* Int8 LM head front end (runtime/lal_q8_kernel.h).
+ * lal_gpu_quantize_x: x[batch][n] fp32 -> xq[batch][n] int8, sx[batch];
+ *   mode 0 = AVX2 build semantics (round-to-nearest-even on the multiple-of-8
+ *   prefix, truncation on the tail), mode 1 = scalar build (truncation).
+ * lal_gpu_lm_head_q8: logits[b][v] = (sx[b]*sw[v]) * (float)dot(xq[b], W[v])
+ *   with exact int32 accumulation; W row-major [vocab][n] int8.  */
+int  lal_gpu_quantize_x(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
+                        int mode, int8_t *d_xq, float *d_sx, void *stream);
+int  lal_gpu_lm_head_q8(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx,
+                        int batch, int n, const int8_t *d_w, const float *d_sw,
+                        int vocab, float *d_logits, int ld, void *stream);
+
+/* Host helper: srand(seed) then n draws of (float)rand()/(float)RAND_MAX
+ * (gpt2 != 0: (float)(rand()%1000000)/1000000.0f), the reference's RNG
+ * stream, written to host memory. */
+void lal_gpu_uniforms_rand(unsigned seed, int n, float *out, int gpt2);
+
+/* Device/stream plumbing so C and ctypes callers need no other HIP binding. */
+int  lal_gpu_device_count(int *count);
+int  lal_gpu_set_device(int device);
+int  lal_gpu_malloc(void **d_ptr, size_t bytes);
+int  lal_gpu_free(void *d_ptr);
+int  lal_gpu_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes, void *stream);
+int  lal_gpu_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes, void *stream);
+int  lal_gpu_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes, void *stream);
+int  lal_gpu_memset(void *d_dst, int value, size_t bytes, void *stream);
+int  lal_gpu_stream_create(void **stream);
+int  lal_gpu_stream_destroy(void *stream);
+int  lal_gpu_stream_sync(void *stream);
+int  lal_gpu_device_sync(void);
+int  lal_gpu_event_create(void **event);
+int  lal_gpu_event_destroy(void *event);
+int  lal_gpu_event_record(void *event, void *stream);
+int  lal_gpu_event_elapsed_ms(float *ms, void *start, void *stop);
+int  lal_gpu_last_hip_error(void);
+const char *lal_gpu_strerror(int code);
+int  lal_gpu_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* LAL_GPU_SAMPLE_H */

@@ -1,0 +1,1732 @@
+// lal_gpu_sample.hip -- MI355X (gfx950) token sampler, int8 LM head and the
+// C ABI declared in include/lal_gpu_sample.h.
+//
+// Sampling path (reference: runtime/lal_sampling.h:46-125,
+// tools/server/qwen7b_server.c:219-295, tools/server/gpt2_server.c:2862-3012,
+// compiler/lal.py:2218-2242).  One workgroup of four wave64s owns one row:
+//
+//   setup     history ids and ban ids go into an LDS hash (id -> occurrence
+//             count, flags, exact processed logit); the exact value of every
+//             history id is computed once from global memory.
+//   stream    the row is read once with coalesced 16-byte loads, 8192 floats
+//             per tile.  Each value gets its cheap upper bound (raw logit plus
+//             bias, -inf when the allow bit is clear); values at or above the
+//             running threshold tau look up the hash for their exact value
+//             (repetition penalty and pre-selection bans only ever lower a
+//             value) and are appended to an LDS candidate buffer.  When the
+//             buffer would overflow, an LDS radix select over buffer + tile
+//             raises tau to the k-th largest value seen so far, which can never
+//             exceed the row's true k-th largest.
+//   select    an LDS radix select over the buffer gives the exact k-th largest
+//             value T (with multiplicity, as the reference's min-heap does).
+//   epilogue  the candidates (value >= T) are sorted by id; nucleus (top-p),
+//             lal_filter_topk bans, softmax and the inverse-CDF draw run over
+//             them with the reference's sequential fp32 order and a bit-exact
+//             restatement of glibc expf.
+//
+// When more than CAP logits tie at the threshold the buffer cannot hold the
+// pool; the row is then finished by re-reading it in id order (rescan).
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <climits>
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "lal_gpu_sample.h"
+#include "lal_gpu_workload.h"
+
+namespace {
+
+constexpr int WG = 256;             // threads per workgroup: 4 wave64
+constexpr int NWAVE = WG / 64;
+constexpr int U4 = 8;               // float4 loads per thread per tile
+constexpr int VPT = 4 * U4;         // values per thread per tile
+constexpr int TILE = WG * VPT;      // 8192 floats per tile
+constexpr int CAP = 2048;           // LDS candidate buffer entries
+constexpr int PER = CAP / WG;       // buffer entries per thread
+constexpr int HBITS = 10;
+constexpr int HSLOTS = 1 << HBITS;  // LDS hash slots (>= 2 x distinct ids)
+constexpr int HCOUNT_MASK = 0xFFFF;
+constexpr int HF_MASKPRE = 1 << 16; // id is -inf before selection
+constexpr int HF_BAN = 1 << 17;     // id is dropped from the top-k pool
+
+static_assert(2 * HSLOTS >= 3 * (LAL_GPU_MAX_HISTORY + LAL_GPU_MAX_BAN_IDS), "hash load <= 2/3");
+static_assert(CAP >= 2 * LAL_GPU_MAX_K, "buffer must hold twice the largest k");
+
+// ---------------------------------------------------------------------------
+// expf as glibc computes it (the reference calls glibc's expf).  This is the
+// published algorithm of glibc 2.27+ / ARM optimized-routines e_expf.c:
+// x*32/ln2 = k + r, 2^(k/32) from a 32-entry table, a cubic for 2^(r/32),
+// evaluated in double.  The fused multiply-adds are the ones the x86-64 FMA
+// build of glibc performs (the range reduction included); this restatement
+// equals glibc expf on all 2^32 float inputs.
+// ---------------------------------------------------------------------------
+__constant__ uint64_t kExp2Tab[32] = {
+    0x3ff0000000000000ull, 0x3fefd9b0d3158574ull, 0x3fefb5586cf9890full, 0x3fef9301d0125b51ull,
+    0x3fef72b83c7d517bull, 0x3fef54873168b9aaull, 0x3fef387a6e756238ull, 0x3fef1e9df51fdee1ull,
+    0x3fef06fe0a31b715ull, 0x3feef1a7373aa9cbull, 0x3feedea64c123422ull, 0x3feece086061892dull,
+    0x3feebfdad5362a27ull, 0x3feeb42b569d4f82ull, 0x3feeab07dd485429ull, 0x3feea47eb03a5585ull,
+    0x3feea09e667f3bcdull, 0x3fee9f75e8ec5f74ull, 0x3feea11473eb0187ull, 0x3feea589994cce13ull,
+    0x3feeace5422aa0dbull, 0x3feeb737b0cdc5e5ull, 0x3feec49182a3f090ull, 0x3feed503b23e255dull,
+    0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
+    0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
+
+__device__ __forceinline__ float glibc_expf(float x)
+{
+    const uint32_t ux = __float_as_uint(x);
+    const uint32_t abstop = (ux >> 20) & 0x7ff;
+    if (abstop >= 0x42b) {                     // |x| >= 88 or nan
+        if (ux == 0xff800000u) return 0.0f;    // -inf
+        if (abstop >= 0x7f8) return x + x;     // +inf or nan
+        if (x > 0x1.62e42ep6f) return __uint_as_float(0x7f800000u);
+        if (x < -0x1.9fe368p6f) return 0.0f;
+    }
+    const double InvLn2N = 0x1.71547652b82fep+0 * 32.0;
+    const double Shift = 0x1.8p+52;
+    const double C0 = 0x1.c6af84b912394p-5 / 32.0 / 32.0 / 32.0;
+    const double C1 = 0x1.ebfce50fac4f3p-3 / 32.0 / 32.0;
+    const double C2 = 0x1.62e42ff0c52d6p-1 / 32.0;
+    const double xd = (double)x;
+    double kd = __fma_rn(InvLn2N, xd, Shift);
+    const uint64_t ki = (uint64_t)__double_as_longlong(kd);
+    kd -= Shift;
+    const double r = __fma_rn(InvLn2N, xd, -kd);
+    uint64_t t = kExp2Tab[ki & 31];
+    t += ki << 47;
+    const double s = __longlong_as_double((long long)t);
+    const double z = __fma_rn(C0, r, C1);
+    const double r2 = r * r;
+    double y = __fma_rn(C2, r, 1.0);
+    y = __fma_rn(z, r2, y);
+    y = y * s;
+    return (float)y;
+}
+
+// Order-preserving float -> uint32 key (-0 folded onto +0; nan never enters).
+__device__ __forceinline__ uint32_t fkey(float f)
+{
+    uint32_t u = __float_as_uint(f);
+    if (u == 0x80000000u) u = 0;
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ float keyf(uint32_t k)
+{
+    return __uint_as_float((k & 0x80000000u) ? (k & 0x7fffffffu) : ~k);
+}
+
+// native vector types for the nontemporal 16-byte loads
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
+__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+
+__device__ __forceinline__ int wave_incl_scan(int v)
+{
+    const int lane = lane_id();
+#pragma unroll
+    for (int d = 1; d < 64; d <<= 1) {
+        int t = __shfl_up(v, d, 64);
+        if (lane >= d) v += t;
+    }
+    return v;
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_min(int v)
+{
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v = min(v, __shfl_xor(v, d, 64));
+    return v;
+}
+
+__device__ __forceinline__ int wave_sum(int v)
+{
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+    return v;
+}
+
+struct Smem {
+    float cval[CAP];      // candidate values (exact processed logits)
+    int cidx[CAP];        // candidate token ids
+    float ep[CAP];        // epilogue scratch: probabilities, prefix sums
+    int hkey[HSLOTS];     // hash: token id or -1
+    int hinfo[HSLOTS];    // occurrence count | HF_* flags
+    float hval[HSLOTS];   // exact processed logit of the id
+    unsigned rhist[256];  // radix histogram
+    int wsum[2][NWAVE];   // block-scan wave totals (double-buffered)
+    float redf[NWAVE];
+    int redi[NWAVE];
+    int redi2[NWAVE];
+    int sel_digit;
+    int sel_rem;
+    int bcast;
+};
+
+struct KArgs {
+    const float *logits;
+    float *logits_w;
+    int ld, V;
+    const int *hist;
+    int hist_ld;
+    const int *hist_len;
+    const uint32_t *allow;
+    int allow_ld;
+    const float *bias;
+    const float *uniforms;
+    int *out_token;
+    float *out_thr;
+    int *out_ncand;
+    int *out_nkept;
+    float *out_sum;
+    int cand_ld;
+    int *cand_ids;
+    float *cand_probs;
+    uint8_t *cand_kept;
+    float *out_hvals;
+    const int *ban_ids;
+    int n_ban;
+    float T, top_p, pen;
+    int k;
+    int variant;
+    unsigned flags;
+    int ban_last, ban_repeat, mask_recent;
+    int greedy;     // greedy path: k = 1, first index among the maxima
+    int apply_pen;  // penalty applied for this variant / greedy state
+    int any_bans;
+};
+
+// block reductions (one barrier each; callers keep control flow uniform)
+__device__ __forceinline__ float block_max(Smem &S, float v)
+{
+    v = wave_max(v);
+    __syncthreads();
+    if (lane_id() == 0) S.redf[wave_id()] = v;
+    __syncthreads();
+    float r = S.redf[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; ++w) r = fmaxf(r, S.redf[w]);
+    return r;
+}
+
+__device__ __forceinline__ int block_min(Smem &S, int v)
+{
+    v = wave_min(v);
+    __syncthreads();
+    if (lane_id() == 0) S.redi[wave_id()] = v;
+    __syncthreads();
+    int r = S.redi[0];
+#pragma unroll
+    for (int w = 1; w < NWAVE; ++w) r = min(r, S.redi[w]);
+    return r;
+}
+
+__device__ __forceinline__ int block_sum(Smem &S, int v)
+{
+    v = wave_sum(v);
+    __syncthreads();
+    if (lane_id() == 0) S.redi2[wave_id()] = v;
+    __syncthreads();
+    int r = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) r += S.redi2[w];
+    return r;
+}
+
+// exclusive block scan; one barrier; wsum must alternate between calls
+__device__ __forceinline__ int block_excl_scan(int v, int &total, int *wsum)
+{
+    const int incl = wave_incl_scan(v);
+    if (lane_id() == 63) wsum[wave_id()] = incl;
+    __syncthreads();
+    int before = 0, tot = 0;
+#pragma unroll
+    for (int w = 0; w < NWAVE; ++w) {
+        const int s = wsum[w];
+        before += (w < wave_id()) ? s : 0;
+        tot += s;
+    }
+    total = tot;
+    return before + incl - v;
+}
+
+// ---------------------------------------------------------------------------
+// LDS hash of the row's history / ban ids
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t hslot(int key)
+{
+    return ((uint32_t)key * 2654435761u) >> (32 - HBITS);
+}
+
+__device__ void hash_insert(Smem &S, int key, int add, int flags)
+{
+    uint32_t s = hslot(key);
+    for (int probe = 0; probe < HSLOTS; ++probe) {
+        const int prev = atomicCAS(&S.hkey[s], -1, key);
+        if (prev == -1 || prev == key) {
+            if (add) atomicAdd(&S.hinfo[s], add);
+            if (flags) atomicOr(&S.hinfo[s], flags);
+            return;
+        }
+        s = (s + 1) & (HSLOTS - 1);
+    }
+}
+
+__device__ __forceinline__ int hash_find(const Smem &S, int key)
+{
+    uint32_t s = hslot(key);
+    for (int probe = 0; probe < HSLOTS; ++probe) {
+        const int k = S.hkey[s];
+        if (k == key) return (int)s;
+        if (k == -1) return -1;
+        s = (s + 1) & (HSLOTS - 1);
+    }
+    return -1;
+}
+
+__device__ __forceinline__ bool allow_bit(const uint32_t *row_bits, int e)
+{
+    return (row_bits[e >> 5] >> (e & 31)) & 1u;
+}
+
+// repetition penalty applied `count` times: x>0 ? x/p : x*p
+// (runtime/lal_sampling.h:63-64, once per history occurrence)
+__device__ __forceinline__ float penalise(float x, int count, float pen)
+{
+    for (int c = 0; c < count; ++c) x = (x > 0.0f) ? x / pen : x * pen;
+    return x;
+}
+
+// ---------------------------------------------------------------------------
+// Block-wide radix select: k-th largest key over the LDS buffer [0, cnt) and
+// the register values v[i] whose bit is set in m.  Requires >= k inputs.
+// ---------------------------------------------------------------------------
+template <int NV>
+__device__ uint32_t block_kth_key(Smem &S, int cnt, const float (&v)[NV], uint64_t m, int k)
+{
+    uint32_t prefix = 0, pmask = 0;
+    int rem = k;
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        S.rhist[threadIdx.x] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if ((m >> i) & 1ull) {
+                const uint32_t key = fkey(v[i]);
+                if ((key & pmask) == prefix) atomicAdd(&S.rhist[(key >> shift) & 255u], 1u);
+            }
+        }
+        for (int j = threadIdx.x; j < cnt; j += WG) {
+            const uint32_t key = fkey(S.cval[j]);
+            if ((key & pmask) == prefix) atomicAdd(&S.rhist[(key >> shift) & 255u], 1u);
+        }
+        __syncthreads();
+        if (threadIdx.x < 64) {
+            const int b0 = 255 - 4 * lane_id();
+            const int h0 = S.rhist[b0], h1 = S.rhist[b0 - 1], h2 = S.rhist[b0 - 2],
+                      h3 = S.rhist[b0 - 3];
+            const int lsum = h0 + h1 + h2 + h3;
+            const int incl = wave_incl_scan(lsum);
+            const int excl = incl - lsum;
+            if (excl < rem && rem <= incl) {
+                int r = rem - excl, d;
+                if (r <= h0) d = b0;
+                else if ((r -= h0) <= h1) d = b0 - 1;
+                else if ((r -= h1) <= h2) d = b0 - 2;
+                else { r -= h2; d = b0 - 3; }
+                S.sel_digit = d;
+                S.sel_rem = r;
+            }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)S.sel_digit << shift;
+        pmask |= 0xFFu << shift;
+        rem = S.sel_rem;
+    }
+    return prefix;
+}
+
+// Sequential fp32 prefix sums over S.ep[0..n) in index order, done by wave 0
+// (lane l of a 64-chunk receives the running sum after element base+l).  The
+// additions happen in exactly the order of the reference's scalar loop.
+// Entries < 0 are "not in the set" markers and are skipped.  Writes the
+// inclusive prefix back into S.ep and returns the total to every thread.
+__device__ float block_seq_prefix(Smem &S, int n, float carry_in)
+{
+    __syncthreads();
+    if (wave_id() == 0) {
+        float acc = carry_in;
+        for (int base = 0; base < n; base += 64) {
+            const int i = base + lane_id();
+            const float e = (i < n) ? S.ep[i] : -1.0f;
+            const unsigned long long live = __ballot(!(e < 0.0f));
+            float pre = acc;
+            if (live) {
+                const int ebits = __float_as_int(e);
+                const int lim = min(64, n - base);
+                const int me = lane_id();
+                for (int l = 0; l < lim; ++l) {
+                    const float el = __int_as_float(__builtin_amdgcn_readlane(ebits, l));
+                    if (!(el < 0.0f)) acc = acc + el;
+                    if (me == l) pre = acc;
+                }
+            }
+            if (i < n) S.ep[i] = pre;
+        }
+        if (lane_id() == 0) S.redf[0] = acc;
+    }
+    __syncthreads();
+    const float tot = S.redf[0];
+    __syncthreads();
+    return tot;
+}
+
+// ---------------------------------------------------------------------------
+// Element addressing for a row: [0, head) scalar head elements, then nb4
+// aligned float4 chunks, then a scalar tail of < 4 elements.  Head and tail
+// ("extra") elements ride along as one more value slot of tile 0.
+// ---------------------------------------------------------------------------
+struct RowGeo {
+    int head, nb4, tail0, ntail, ntiles;
+};
+
+__device__ __forceinline__ RowGeo row_geo(const float *row, int V)
+{
+    RowGeo g;
+    const int mis = (int)(((uintptr_t)row >> 2) & 3);
+    g.head = min((4 - mis) & 3, V);
+    g.nb4 = (V - g.head) >> 2;
+    g.tail0 = g.head + 4 * g.nb4;
+    g.ntail = V - g.tail0;
+    g.ntiles = max(1, (g.nb4 + TILE / 4 - 1) / (TILE / 4));
+    return g;
+}
+
+__device__ __forceinline__ int extra_elem(const RowGeo &g, int t)
+{
+    if (t < g.head) return t;
+    if (t < g.head + g.ntail) return g.tail0 + (t - g.head);
+    return -1;
+}
+
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__device__ __forceinline__ float upper_bound(const KArgs &A, const uint32_t *abits, int e, float x)
+{
+    float y = x;
+    if (HAS_BIAS) y = y + A.bias[e];
+    if (HAS_ALLOW) {
+        if (!allow_bit(abits, e)) y = -INFINITY;
+    }
+    return y;
+}
+
+// exact processed value for a value that passed the upper-bound filter
+__device__ __forceinline__ float exact_value(const Smem &S, bool use_hash, int e, float yhat)
+{
+    if (use_hash) {
+        const int s = hash_find(S, e);
+        if (s >= 0) return S.hval[s];
+    }
+    return yhat;
+}
+
+__device__ __forceinline__ bool passes(float y, float tau, bool strict)
+{
+    return strict ? (y > tau) : (y >= tau);
+}
+
+// Load tile `t` of the row into y[0..VPT) (+ y[VPT] for the extra slot),
+// replacing each value by its exact processed value when it passes (tau,
+// strict), and NaN when it is out of range or fails.  Returns the pass mask.
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__device__ __forceinline__ uint64_t load_tile(const KArgs &A, const Smem &S, const float *row,
+                                              const uint32_t *abits, const RowGeo &g, int t,
+                                              float tau, bool strict, bool use_hash,
+                                              float (&y)[VPT + 1])
+{
+    const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
+    f32x4 xv[U4];
+#pragma unroll
+    for (int u = 0; u < U4; ++u) {
+        const int q = t * (TILE / 4) + u * WG + (int)threadIdx.x;
+        if (q < g.nb4) xv[u] = __builtin_nontemporal_load(row4 + q);
+        else xv[u] = f32x4{NAN, NAN, NAN, NAN};
+    }
+    uint64_t m = 0;
+#pragma unroll
+    for (int u = 0; u < U4; ++u) {
+        const int q = t * (TILE / 4) + u * WG + (int)threadIdx.x;
+        const int e0 = g.head + 4 * q;
+        const float xs[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            const int i = 4 * u + c;
+            float yy = xs[c];
+            if (q < g.nb4) {
+                yy = upper_bound<HAS_BIAS, HAS_ALLOW>(A, abits, e0 + c, yy);
+                if (passes(yy, tau, strict)) {
+                    yy = exact_value(S, use_hash, e0 + c, yy);
+                    if (passes(yy, tau, strict)) m |= 1ull << i;
+                }
+            }
+            y[i] = yy;
+        }
+    }
+    // extra slot (head / tail elements) in tile 0
+    y[VPT] = NAN;
+    if (t == 0) {
+        const int e = extra_elem(g, threadIdx.x);
+        if (e >= 0) {
+            float yy = upper_bound<HAS_BIAS, HAS_ALLOW>(A, abits, e, row[e]);
+            if (passes(yy, tau, strict)) {
+                yy = exact_value(S, use_hash, e, yy);
+                if (passes(yy, tau, strict)) m |= 1ull << VPT;
+            }
+            y[VPT] = yy;
+        }
+    }
+    return m;
+}
+
+__device__ __forceinline__ int tile_elem(const RowGeo &g, int t, int i)
+{
+    if (i == VPT) return extra_elem(g, threadIdx.x);
+    const int u = i >> 2, c = i & 3;
+    const int q = t * (TILE / 4) + u * WG + (int)threadIdx.x;
+    return g.head + 4 * q + c;
+}
+
+// ---------------------------------------------------------------------------
+// Rescan path: finish the row by re-reading it in id order (used when more
+// than CAP logits tie at the threshold, so the pool is not in LDS).
+// ---------------------------------------------------------------------------
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__device__ float rescan_value(const KArgs &A, const Smem &S, const float *row, const uint32_t *abits,
+                              bool use_hash, int e, float x)
+{
+    const float yh = upper_bound<HAS_BIAS, HAS_ALLOW>(A, abits, e, x);
+    return exact_value(S, use_hash, e, yh);
+}
+
+// Fills S.ep[0..n) for the element chunk starting at `e0` (n consecutive ids
+// handled as: thread tid owns ids e0+4tid .. e0+4tid+3 for float4 chunks, or
+// e0+tid for scalar chunks) with kept ? e : -1.
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__device__ void rescan_chunk_e(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
+                               bool use_hash, float T, bool use_keep_ban, float mx, int e_begin,
+                               int n, bool vec)
+{
+    __syncthreads();
+    if (vec) {
+        const int base = 4 * threadIdx.x;
+        if (base < n) {
+            const float4 xv = *reinterpret_cast<const float4 *>(row + e_begin + base);
+            const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                const int e = e_begin + base + c;
+                const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, xs[c]);
+                bool kept = (yv >= T);
+                if (kept && use_keep_ban) {
+                    const int s = hash_find(S, e);
+                    if (s >= 0 && (S.hinfo[s] & HF_BAN)) kept = false;
+                }
+                S.ep[base + c] = kept ? glibc_expf((yv - mx) / A.T) : -1.0f;
+            }
+        }
+    } else if ((int)threadIdx.x < n) {
+        const int e = e_begin + threadIdx.x;
+        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
+        bool kept = (yv >= T);
+        if (kept && use_keep_ban) {
+            const int s = hash_find(S, e);
+            if (s >= 0 && (S.hinfo[s] & HF_BAN)) kept = false;
+        }
+        S.ep[threadIdx.x] = kept ? glibc_expf((yv - mx) / A.T) : -1.0f;
+    }
+}
+
+struct RescanStats {
+    int n_cand, n_kept;
+    float max_kept;     // max over the set, plain max (no -1e30 floor)
+    int first_kept;     // smallest id in the set
+    int first_max_kept; // smallest id attaining max_kept
+};
+
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__device__ RescanStats rescan_stats(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
+                                    const RowGeo &g, bool use_hash, float T, bool use_ban)
+{
+    int nc = 0, nk = 0, first = INT_MAX;
+    float mk = -INFINITY;
+    // pass 1: counts, max and first id
+    for (int e = threadIdx.x; e < A.V; e += WG) {
+        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
+        if (!(yv >= T)) continue;
+        nc++;
+        if (use_ban) {
+            const int s = hash_find(S, e);
+            if (s >= 0 && (S.hinfo[s] & HF_BAN)) continue;
+        }
+        nk++;
+        mk = fmaxf(mk, yv);
+        first = min(first, e);
+    }
+    RescanStats st;
+    st.n_cand = block_sum(S, nc);
+    st.n_kept = block_sum(S, nk);
+    st.max_kept = block_max(S, mk);
+    st.first_kept = block_min(S, first);
+    int fm = INT_MAX;
+    for (int e = threadIdx.x; e < A.V; e += WG) {
+        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
+        if (!(yv >= T) || !(yv == st.max_kept)) continue;
+        if (use_ban) {
+            const int s = hash_find(S, e);
+            if (s >= 0 && (S.hinfo[s] & HF_BAN)) continue;
+        }
+        fm = min(fm, e);
+    }
+    st.first_max_kept = block_min(S, fm);
+    return st;
+}
+
+// Sequential sum (draw == false) or draw (draw == true) over the row in id
+// order.  Returns the sum, or via *token the first kept id with r <= acc.
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__device__ float rescan_sequential(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
+                                   const RowGeo &g, bool use_hash, float T, bool use_ban, float mx,
+                                   bool draw, float r, int *token)
+{
+    float acc = 0.0f;
+    int found = -1;
+    // chunk list in id order: head, body float4 chunks (1024 ids each), tail
+    auto run = [&](int e_begin, int n, bool vec) {
+        if (n <= 0) return;
+        rescan_chunk_e<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, mx, e_begin, n, vec);
+        __syncthreads();
+        if (wave_id() == 0 && found < 0) {
+            for (int base = 0; base < n && found < 0; base += 64) {
+                const int i = base + lane_id();
+                const float e = (i < n) ? S.ep[i] : -1.0f;
+                if (!__ballot(!(e < 0.0f))) continue;
+                const int ebits = __float_as_int(e);
+                const int lim = min(64, n - base);
+                for (int l = 0; l < lim; ++l) {
+                    const float el = __int_as_float(__builtin_amdgcn_readlane(ebits, l));
+                    if (el < 0.0f) continue;
+                    acc = acc + el;
+                    if (draw && r <= acc) { found = e_begin + base + l; break; }
+                }
+            }
+        }
+        if (wave_id() == 0 && lane_id() == 0) S.bcast = found;
+        __syncthreads();
+        found = S.bcast;
+    };
+    run(0, g.head, false);
+    for (int t = 0; t < (g.nb4 + WG - 1) / WG && found < 0; ++t) {
+        const int q0 = t * WG;
+        const int nq = min(WG, g.nb4 - q0);
+        run(g.head + 4 * q0, 4 * nq, true);
+    }
+    if (found < 0) run(g.tail0, g.ntail, false);
+    if (wave_id() == 0 && lane_id() == 0) S.redf[0] = acc;
+    __syncthreads();
+    const float tot = S.redf[0];
+    __syncthreads();
+    if (token) *token = found;
+    return tot;
+}
+
+// ---------------------------------------------------------------------------
+// The sampler kernel: one workgroup per row.
+// ---------------------------------------------------------------------------
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
+{
+    __shared__ Smem S;
+    const int b = blockIdx.x;
+    const int tid = threadIdx.x;
+    const int V = A.V;
+    const float *row = A.logits + (size_t)b * A.ld;
+    const uint32_t *abits = HAS_ALLOW ? A.allow + (size_t)b * A.allow_ld : nullptr;
+    const int *hrow = A.hist ? A.hist + (size_t)b * A.hist_ld : nullptr;
+    int nh = 0;
+    if (hrow) {
+        nh = A.hist_len ? A.hist_len[b] : A.hist_ld;
+        nh = max(0, min(nh, A.hist_ld));
+    }
+
+    // ---- setup: hash of history / ban ids -------------------------------
+    for (int s = tid; s < HSLOTS; s += WG) {
+        S.hkey[s] = -1;
+        S.hinfo[s] = 0;
+    }
+    __syncthreads();
+    for (int i = tid; i < nh; i += WG) {
+        const int t = hrow[i];
+        if (t < 0 || t >= V) continue;
+        int flags = 0;
+        if (A.mask_recent > 0 && i >= nh - A.mask_recent) flags |= HF_MASKPRE;
+        if (A.ban_last && i == nh - 1) flags |= HF_BAN;
+        if (A.ban_repeat > 0 && i >= nh - A.ban_repeat) flags |= HF_BAN;
+        hash_insert(S, t, A.apply_pen ? 1 : 0, flags);
+    }
+    for (int i = tid; i < A.n_ban; i += WG) {
+        const int t = A.ban_ids[i];
+        if (t >= 0 && t < V) hash_insert(S, t, 0, HF_BAN);
+    }
+    __syncthreads();
+    int nocc = 0;
+    for (int s = tid; s < HSLOTS; s += WG) {
+        const int key = S.hkey[s];
+        if (key < 0) continue;
+        nocc++;
+        const int info = S.hinfo[s];
+        float yv = penalise(row[key], info & HCOUNT_MASK, A.pen);
+        if (HAS_BIAS) yv = yv + A.bias[key];
+        if (HAS_ALLOW && !allow_bit(abits, key)) yv = -INFINITY;
+        if (info & HF_MASKPRE) yv = -INFINITY;
+        S.hval[s] = yv;
+    }
+    const bool use_hash = block_sum(S, nocc) > 0;
+
+    // ---- stream the row -----------------------------------------------------
+    const RowGeo g = row_geo(row, V);
+    const int k = A.greedy ? 1 : min(max(A.k, 1), V);
+    float tau = -INFINITY;
+    bool strict = false;
+    bool tie = false;
+    float tie_val = -INFINITY;
+    int cnt = 0;
+
+    for (int t = 0; t < g.ntiles; ++t) {
+        float y[VPT + 1];
+        uint64_t m = load_tile<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, t, tau, strict, use_hash, y);
+        const int c = __popcll(m);
+        int total;
+        const int off = block_excl_scan(c, total, S.wsum[t & 1]);
+        if (cnt + total <= CAP) {
+            int pos = cnt + off;
+#pragma unroll
+            for (int i = 0; i <= VPT; ++i) {
+                if ((m >> i) & 1ull) {
+                    S.cval[pos] = y[i];
+                    S.cidx[pos] = tile_elem(g, t, i);
+                    pos++;
+                }
+            }
+            cnt += total;
+        } else {
+            // overflow: raise tau to the k-th largest of buffer + this tile
+            const uint32_t K = block_kth_key<VPT + 1>(S, cnt, y, m, k);
+            const float tk = keyf(K);
+            // entries >= tk in buffer and tile
+            float bv[PER];
+            int bi[PER];
+            int nb_ge = 0, nb_gt = 0;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int j = tid + r * WG;
+                bv[r] = (j < cnt) ? S.cval[j] : NAN;
+                bi[r] = (j < cnt) ? S.cidx[j] : -1;
+                nb_ge += (bv[r] >= tk);
+                nb_gt += (bv[r] > tk);
+            }
+            int nt_ge = 0, nt_gt = 0;
+#pragma unroll
+            for (int i = 0; i <= VPT; ++i) {
+                if ((m >> i) & 1ull) {
+                    nt_ge += (y[i] >= tk);
+                    nt_gt += (y[i] > tk);
+                }
+            }
+            const int n_ge = block_sum(S, nb_ge + nt_ge);
+            const bool use_strict = n_ge > CAP;
+            const int mine = use_strict ? (nb_gt + nt_gt) : (nb_ge + nt_ge);
+            int tot2;
+            const int off2 = block_excl_scan(mine, tot2, S.wsum[(t + 1) & 1]);
+            __syncthreads();  // every thread has its buffer entries in registers
+            int pos = off2;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                if (use_strict ? (bv[r] > tk) : (bv[r] >= tk)) {
+                    S.cval[pos] = bv[r];
+                    S.cidx[pos] = bi[r];
+                    pos++;
+                }
+            }
+#pragma unroll
+            for (int i = 0; i <= VPT; ++i) {
+                if (((m >> i) & 1ull) && (use_strict ? (y[i] > tk) : (y[i] >= tk))) {
+                    S.cval[pos] = y[i];
+                    S.cidx[pos] = tile_elem(g, t, i);
+                    pos++;
+                }
+            }
+            cnt = tot2;
+            tau = tk;
+            strict = use_strict;
+            if (use_strict) {
+                tie = true;
+                tie_val = tk;
+            }
+            __syncthreads();
+        }
+    }
+    __syncthreads();
+
+    // ---- exact threshold ------------------------------------------------
+    float T;
+    bool rescan = false;
+    if (cnt >= k) {
+        const float none[VPT + 1] = {};
+        const uint32_t K = block_kth_key<VPT + 1>(S, cnt, none, 0ull, k);
+        T = keyf(K);
+    } else if (tie) {
+        T = tie_val;       // fewer than k stored above the tie value
+        rescan = true;
+    } else {
+        T = -INFINITY;     // fewer than k non-nan values in the row
+        if (cnt == 0) rescan = true;
+    }
+
+    const bool top_p_on = (A.top_p > 0.0f && A.top_p < 1.0f) && !A.greedy;
+    const float u = A.uniforms ? A.uniforms[b] : 0.0f;
+    int token = V - 1;
+    int n_cand = 0, n_kept = 0;
+    float sum2 = 0.0f;
+
+    if (!rescan) {
+        // ---- compact candidates (>= T) to the front, then sort by id -------
+        float bv[PER];
+        int bi[PER];
+        int mine = 0;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int j = tid + r * WG;
+            bv[r] = (j < cnt) ? S.cval[j] : NAN;
+            bi[r] = (j < cnt) ? S.cidx[j] : -1;
+            mine += (bv[r] >= T);
+        }
+        int nc;
+        const int off = block_excl_scan(mine, nc, S.wsum[0]);
+        __syncthreads();
+        int pos = off;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            if (bv[r] >= T) {
+                S.cval[pos] = bv[r];
+                S.cidx[pos] = bi[r];
+                pos++;
+            }
+        }
+        __syncthreads();
+        n_cand = nc;
+        // rank sort by id (ids are distinct)
+        int rk[PER];
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int j = tid + r * WG;
+            rk[r] = -1;
+            if (j < nc) {
+                bv[r] = S.cval[j];
+                bi[r] = S.cidx[j];
+                int rank = 0;
+                for (int q = 0; q < nc; ++q) rank += (S.cidx[q] < bi[r]);
+                rk[r] = rank;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            if (rk[r] >= 0) {
+                S.cval[rk[r]] = bv[r];
+                S.cidx[rk[r]] = bi[r];
+            }
+        }
+        __syncthreads();
+
+        if (A.greedy) {
+            token = S.cidx[0];
+            n_kept = 1;
+        } else {
+            // per-entry state, entry j = tid + r*WG, in id order
+            float yv[PER];
+            bool nuc[PER], ban[PER], kept[PER];
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int j = tid + r * WG;
+                yv[r] = (j < nc) ? S.cval[j] : NAN;
+                nuc[r] = (j < nc);
+                ban[r] = false;
+                if (j < nc && A.any_bans) {
+                    const int s = hash_find(S, S.cidx[j]);
+                    ban[r] = (s >= 0) && (S.hinfo[s] & HF_BAN);
+                }
+            }
+            if (top_p_on) {
+                // gpt2_server.c:2908-2955: probabilities over the pool
+                float lm = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < PER; ++r)
+                    if (tid + r * WG < nc) lm = fmaxf(lm, yv[r]);
+                float amax = block_max(S, lm);
+                if (!(amax > -1e30f)) amax = -1e30f;
+                float e1[PER];
+#pragma unroll
+                for (int r = 0; r < PER; ++r) {
+                    const int j = tid + r * WG;
+                    e1[r] = (j < nc) ? glibc_expf((yv[r] - amax) / A.T) : 0.0f;
+                    if (j < nc) S.ep[j] = e1[r];
+                }
+                const float se = block_seq_prefix(S, nc, 0.0f);
+                const float inv = 1.0f / (se + 1e-12f);
+                float pr[PER];
+#pragma unroll
+                for (int r = 0; r < PER; ++r) {
+                    const int j = tid + r * WG;
+                    pr[r] = e1[r] * inv;
+                    if (j < nc) S.ep[j] = pr[r];
+                }
+                __syncthreads();
+                // stable descending rank: larger p first, ties by id
+                int prk[PER];
+#pragma unroll
+                for (int r = 0; r < PER; ++r) {
+                    const int j = tid + r * WG;
+                    prk[r] = -1;
+                    if (j < nc) {
+                        int rank = 0;
+                        for (int q = 0; q < nc; ++q) {
+                            const float pq = S.ep[q];
+                            rank += (pq > pr[r]) || (pq == pr[r] && q < j);
+                        }
+                        prk[r] = rank;
+                    }
+                }
+                __syncthreads();
+#pragma unroll
+                for (int r = 0; r < PER; ++r)
+                    if (prk[r] >= 0) S.ep[prk[r]] = pr[r];
+                __syncthreads();
+                // inclusive cumulative cutoff in sorted order
+                if (wave_id() == 0) {
+                    float cum = 0.0f;
+                    int cut = -1;
+                    for (int base = 0; base < nc && cut < 0; base += 64) {
+                        const int i = base + lane_id();
+                        const int pb = __float_as_int((i < nc) ? S.ep[i] : 0.0f);
+                        const int lim = min(64, nc - base);
+                        for (int l = 0; l < lim; ++l) {
+                            cum = cum + __int_as_float(__builtin_amdgcn_readlane(pb, l));
+                            if (cum >= A.top_p) { cut = base + l; break; }
+                        }
+                    }
+                    if (lane_id() == 0) S.bcast = (cut < 0) ? nc - 1 : cut;
+                }
+                __syncthreads();
+                const int cut = S.bcast;
+#pragma unroll
+                for (int r = 0; r < PER; ++r) nuc[r] = (prk[r] >= 0) && (prk[r] <= cut);
+            }
+            // bans on the nucleus, restore the top-k pool if all dropped
+            int lk = 0;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                kept[r] = nuc[r] && !ban[r];
+                lk += kept[r];
+            }
+            n_kept = block_sum(S, lk);
+            if (n_kept == 0) {
+#pragma unroll
+                for (int r = 0; r < PER; ++r) kept[r] = (tid + r * WG < nc);
+                n_kept = nc;
+            }
+            // softmax over the kept set (qwen7b_server.c:275-284)
+            float lm = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < PER; ++r)
+                if (kept[r]) lm = fmaxf(lm, yv[r]);
+            const float kmax = block_max(S, lm);
+            const float mx = (kmax > -1e30f) ? kmax : -1e30f;
+            float e2[PER];
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int j = tid + r * WG;
+                e2[r] = kept[r] ? glibc_expf((yv[r] - mx) / A.T) : 0.0f;
+                if (j < nc) S.ep[j] = kept[r] ? e2[r] : -1.0f;
+            }
+            sum2 = block_seq_prefix(S, nc, 0.0f);
+            if (A.variant == LAL_GPU_VARIANT_FILTERED && sum2 <= 0.0f) {
+                // argmax over the kept set (qwen7b_server.c:285-286)
+                int cand = INT_MAX;
+#pragma unroll
+                for (int r = 0; r < PER; ++r)
+                    if (kept[r] && yv[r] == kmax && kmax > -1e30f) cand = min(cand, tid + r * WG);
+                const int j = block_min(S, cand);
+                token = (j == INT_MAX) ? 0 : S.cidx[j];
+            } else {
+                const float rr = u * sum2;
+                if ((A.flags & LAL_GPU_F_DRAW_GPT2) && rr == 0.0f) {
+                    token = 0;
+                } else {
+                    int cand = INT_MAX;
+#pragma unroll
+                    for (int r = 0; r < PER; ++r)
+                        if (kept[r] && rr <= S.ep[tid + r * WG]) cand = min(cand, tid + r * WG);
+                    const int j = block_min(S, cand);
+                    token = (j == INT_MAX) ? V - 1 : S.cidx[j];
+                }
+            }
+            // optional candidate outputs
+            if (A.cand_ld > 0) {
+#pragma unroll
+                for (int r = 0; r < PER; ++r) {
+                    const int j = tid + r * WG;
+                    if (j < nc && j < A.cand_ld) {
+                        const size_t o = (size_t)b * A.cand_ld + j;
+                        if (A.cand_ids) A.cand_ids[o] = S.cidx[j];
+                        if (A.cand_kept) A.cand_kept[o] = kept[r] ? 1 : 0;
+                        if (A.cand_probs) A.cand_probs[o] = kept[r] ? e2[r] / sum2 : 0.0f;
+                    }
+                }
+            }
+        }
+        if (A.greedy && A.cand_ld > 0) {
+            for (int j = tid; j < nc && j < A.cand_ld; j += WG) {
+                const size_t o = (size_t)b * A.cand_ld + j;
+                if (A.cand_ids) A.cand_ids[o] = S.cidx[j];
+                if (A.cand_kept) A.cand_kept[o] = (j == 0);
+                if (A.cand_probs) A.cand_probs[o] = (j == 0) ? 1.0f : 0.0f;
+            }
+        }
+    } else {
+        // ---- rescan: the pool is larger than the LDS buffer -------------
+        if (top_p_on) {
+            token = -1;  // not supported: nucleus over a pool above CAP tokens
+            n_cand = -1;
+        } else {
+            RescanStats st = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, use_hash, T,
+                                                              A.any_bans && !A.greedy);
+            bool use_ban = A.any_bans && !A.greedy;
+            if (use_ban && st.n_kept == 0) {
+                use_ban = false;  // restore the pool
+                st = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, use_hash, T, false);
+            }
+            n_cand = st.n_cand;
+            n_kept = st.n_kept;
+            if (A.greedy) {
+                token = st.first_kept;
+                n_kept = 1;
+            } else {
+                const float mx = (st.max_kept > -1e30f) ? st.max_kept : -1e30f;
+                sum2 = rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, use_hash, T,
+                                                              use_ban, mx, false, 0.0f, nullptr);
+                if (A.variant == LAL_GPU_VARIANT_FILTERED && sum2 <= 0.0f) {
+                    token = (st.max_kept > -1e30f) ? st.first_max_kept : 0;
+                } else {
+                    const float rr = u * sum2;
+                    if ((A.flags & LAL_GPU_F_DRAW_GPT2) && rr == 0.0f) {
+                        token = 0;
+                    } else {
+                        int f = -1;
+                        rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, use_hash, T,
+                                                               use_ban, mx, true, rr, &f);
+                        token = (f < 0) ? V - 1 : f;
+                    }
+                }
+            }
+        }
+    }
+
+    if (tid == 0) {
+        A.out_token[b] = token;
+        if (A.out_thr) A.out_thr[b] = T;
+        if (A.out_ncand) A.out_ncand[b] = n_cand;
+        if (A.out_nkept) A.out_nkept[b] = n_kept;
+        if (A.out_sum) A.out_sum[b] = sum2;
+    }
+
+    // ---- in-place penalty side effect / penalised history values --------
+    if ((A.flags & LAL_GPU_F_WRITEBACK) || A.out_hvals) {
+        __syncthreads();
+        for (int s = tid; s < HSLOTS; s += WG) {
+            const int key = S.hkey[s];
+            if (key >= 0) S.hval[s] = penalise(row[key], S.hinfo[s] & HCOUNT_MASK, A.pen);
+        }
+        __syncthreads();
+        if (A.out_hvals) {
+            for (int i = tid; i < nh; i += WG) {
+                const int t = hrow[i];
+                if (t >= 0 && t < V) {
+                    const int s = hash_find(S, t);
+                    A.out_hvals[(size_t)b * A.hist_ld + i] = S.hval[s];
+                }
+            }
+        }
+        if (A.flags & LAL_GPU_F_WRITEBACK) {
+            for (int s = tid; s < HSLOTS; s += WG) {
+                const int key = S.hkey[s];
+                if (key >= 0 && (S.hinfo[s] & HCOUNT_MASK))
+                    A.logits_w[(size_t)b * A.ld + key] = S.hval[s];
+            }
+        }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// int8 LM head front end (runtime/lal_q8_kernel.h:375-543)
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void quantize_x_kernel(const float *x, int n, int mode,
+                                                         int8_t *xq, float *sx)
+{
+    __shared__ float red[4];
+    const int b = blockIdx.x;
+    const float *xr = x + (size_t)b * n;
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(xr[i]));
+    m = wave_max(m);
+    if (lane_id() == 0) red[wave_id()] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float scale = m / 127.0f;
+    if (scale < 1e-8f) scale = 1e-8f;
+    const float inv = 1.0f / scale;
+    const int rne_end = (mode == 0) ? (n & ~7) : 0;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float s = xr[i] * inv;
+        int q = (i < rne_end) ? (int)__builtin_rintf(s) : (int)s;
+        q = min(127, max(-127, q));
+        xq[(size_t)b * n + i] = (int8_t)q;
+    }
+    if (threadIdx.x == 0) sx[b] = scale;
+}
+
+// GEMV/GEMM-by-rows: each wave computes LMH_ROWS vocab rows for all batch rows
+// with v_dot4 int8 dot products (exact int32 accumulation).
+constexpr int LMH_ROWS = 4;
+constexpr int LMH_MAXB = 8;
+
+template <int NB>
+__global__ __launch_bounds__(256) void lm_head_dot4_kernel(const int8_t *xq, const float *sx, int n,
+                                                           const int8_t *w, const float *sw, int V,
+                                                           float *logits, int ld, int b0)
+{
+    const int wave = blockIdx.x * 4 + wave_id();
+    const int v0 = wave * LMH_ROWS;
+    if (v0 >= V) return;
+    const int lane = lane_id();
+    int acc[LMH_ROWS][NB];
+#pragma unroll
+    for (int r = 0; r < LMH_ROWS; ++r)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) acc[r][j] = 0;
+    const int n16 = n >> 4;  // 16-byte chunks
+    for (int c = lane; c < n16; c += 64) {
+        int4 xv[NB];
+#pragma unroll
+        for (int j = 0; j < NB; ++j)
+            xv[j] = *reinterpret_cast<const int4 *>(xq + (size_t)(b0 + j) * n + 16 * c);
+#pragma unroll
+        for (int r = 0; r < LMH_ROWS; ++r) {
+            if (v0 + r >= V) break;
+            const i32x4 wv = __builtin_nontemporal_load(
+                reinterpret_cast<const i32x4 *>(w + (size_t)(v0 + r) * n + 16 * c));
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                int a = acc[r][j];
+                a = __builtin_amdgcn_sdot4(wv.x, xv[j].x, a, false);
+                a = __builtin_amdgcn_sdot4(wv.y, xv[j].y, a, false);
+                a = __builtin_amdgcn_sdot4(wv.z, xv[j].z, a, false);
+                a = __builtin_amdgcn_sdot4(wv.w, xv[j].w, a, false);
+                acc[r][j] = a;
+            }
+        }
+    }
+    // tail (n not a multiple of 16)
+    for (int i = 16 * n16 + lane; i < n; i += 64) {
+#pragma unroll
+        for (int r = 0; r < LMH_ROWS; ++r) {
+            if (v0 + r >= V) break;
+            const int wv = w[(size_t)(v0 + r) * n + i];
+#pragma unroll
+            for (int j = 0; j < NB; ++j) acc[r][j] += wv * (int)xq[(size_t)(b0 + j) * n + i];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < LMH_ROWS; ++r)
+#pragma unroll
+        for (int j = 0; j < NB; ++j) {
+            int a = acc[r][j];
+#pragma unroll
+            for (int d = 32; d >= 1; d >>= 1) a += __shfl_xor(a, d, 64);
+            acc[r][j] = a;
+        }
+    if (lane < LMH_ROWS * NB) {
+        const int r = lane / NB, j = lane % NB;
+        int dot = 0;
+#pragma unroll
+        for (int rr = 0; rr < LMH_ROWS; ++rr)
+#pragma unroll
+            for (int jj = 0; jj < NB; ++jj)
+                if (rr == r && jj == j) dot = acc[rr][jj];
+        if (v0 + r < V)
+            logits[(size_t)(b0 + j) * ld + v0 + r] = (sx[b0 + j] * sw[v0 + r]) * (float)dot;
+    }
+}
+
+// Rows whose length is not a multiple of 16 bytes: one wave per vocab row,
+// byte loads, same exact int32 accumulation.
+__global__ __launch_bounds__(256) void lm_head_scalar_kernel(const int8_t *xq, const float *sx, int n,
+                                                             const int8_t *w, const float *sw, int V,
+                                                             float *logits, int ld, int batch)
+{
+    const int v = blockIdx.x * 4 + wave_id();
+    if (v >= V) return;
+    const int8_t *wr = w + (size_t)v * n;
+    for (int b = 0; b < batch; ++b) {
+        int a = 0;
+        for (int i = lane_id(); i < n; i += 64) a += (int)wr[i] * (int)xq[(size_t)b * n + i];
+#pragma unroll
+        for (int d = 32; d >= 1; d >>= 1) a += __shfl_xor(a, d, 64);
+        if (lane_id() == 0) logits[(size_t)b * ld + v] = (sx[b] * sw[v]) * (float)a;
+    }
+}
+
+// ---------------------------------------------------------------------------
+// synthetic workloads (benchmarks / tests)
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint64_t mix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+__device__ __forceinline__ float u01(uint64_t h) { return (float)(h >> 40) * (1.0f / 16777216.0f); }
+
+__device__ __forceinline__ float gauss(uint64_t h)
+{
+    const float u1 = ((float)(h >> 40) + 0.5f) * (1.0f / 16777216.0f);
+    const float u2 = (float)((h >> 16) & 0xFFFFFF) * (1.0f / 16777216.0f);
+    return sqrtf(-2.0f * logf(u1)) * cospif(2.0f * u2);
+}
+
+__global__ void synth_gauss_kernel(float *out, int V, int ld, uint64_t seed, float sigma,
+                                   float offr, int nout, float outv)
+{
+    const int b = blockIdx.y;
+    const uint64_t rs = mix64(seed ^ mix64((uint64_t)b + 0x1234567ull));
+    const float off = offr != 0.0f ? (u01(mix64(rs ^ 0xABCDEFull)) * 2.0f - 1.0f) * offr : 0.0f;
+    for (int v = blockIdx.x * blockDim.x + threadIdx.x; v < V; v += gridDim.x * blockDim.x) {
+        float x = sigma * gauss(mix64(rs + (uint64_t)v)) + off;
+        out[(size_t)b * ld + v] = x;
+    }
+    __syncthreads();
+    if (blockIdx.x == 0 && (int)threadIdx.x < nout) {
+        const int v = (int)(mix64(rs ^ (0x5151ull + threadIdx.x)) % (uint64_t)V);
+        out[(size_t)b * ld + v] = outv;
+    }
+}
+
+__global__ void synth_zipf_kernel(float *out, int V, int ld, uint64_t seed, float slope, float noise)
+{
+    const int b = blockIdx.y;
+    const uint64_t rs = mix64(seed ^ mix64((uint64_t)b + 0x777ull));
+    // rank(v) = (a*v + c) mod V + 1 with gcd(a, V) = 1 (a odd, not multiple of 3)
+    uint64_t a = (mix64(rs) % (uint64_t)V) | 1ull;
+    while ((V % 3 == 0 && a % 3 == 0) || (V % 7 == 0 && a % 7 == 0) || (V % 11 == 0 && a % 11 == 0) ||
+           (V % 5 == 0 && a % 5 == 0) || (V % 13 == 0 && a % 13 == 0))
+        a += 2;
+    const uint64_t c = mix64(rs + 1) % (uint64_t)V;
+    for (int v = blockIdx.x * blockDim.x + threadIdx.x; v < V; v += gridDim.x * blockDim.x) {
+        const uint64_t rank = (a * (uint64_t)v + c) % (uint64_t)V + 1;
+        const float x = -slope * logf((float)rank) + noise * gauss(mix64(rs + 77 + (uint64_t)v));
+        out[(size_t)b * ld + v] = x;
+    }
+}
+
+__global__ void synth_bits_kernel(uint32_t *out, int V, int wld, uint64_t seed, float p)
+{
+    const int b = blockIdx.y;
+    const int nw = (V + 31) / 32;
+    for (int w = blockIdx.x * blockDim.x + threadIdx.x; w < wld; w += gridDim.x * blockDim.x) {
+        uint32_t bits = 0;
+        if (w < nw) {
+            for (int j = 0; j < 32; ++j) {
+                const int v = 32 * w + j;
+                if (v < V && u01(mix64(seed ^ mix64(((uint64_t)b << 32) + (uint64_t)v))) < p)
+                    bits |= 1u << j;
+            }
+        }
+        out[(size_t)b * wld + w] = bits;
+    }
+}
+
+__global__ void synth_int8_kernel(int8_t *out, size_t n, uint64_t seed, int lo, int hi)
+{
+    const uint64_t span = (uint64_t)(hi - lo + 1);
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = (int8_t)(lo + (int)(mix64(seed + i) % span));
+}
+
+__global__ void synth_uniform_kernel(float *out, size_t n, uint64_t seed, float lo, float hi)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = lo + (hi - lo) * u01(mix64(seed + i));
+}
+
+__global__ void synth_normal_kernel(float *out, size_t n, uint64_t seed, float sigma)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = sigma * gauss(mix64(seed + i));
+}
+
+__global__ void synth_ids_kernel(int *out, size_t n, uint64_t seed, int V)
+{
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
+        out[i] = (int)(mix64(seed + i) % (uint64_t)V);
+}
+
+// expf restatement exposed for the exhaustive check against glibc
+__global__ void expf_check_kernel(uint32_t first_hi, int nhi, uint64_t *out)
+{
+    // one block per 65536-input chunk; out[chunk] = order-sensitive hash of results
+    const uint32_t hi = first_hi + blockIdx.x;
+    uint64_t h = 0;
+    for (uint32_t lo = threadIdx.x; lo < 65536u; lo += blockDim.x) {
+        const uint32_t ux = (hi << 16) | lo;
+        const float r = glibc_expf(__uint_as_float(ux));
+        uint32_t rb = __float_as_uint(r);
+        if (r != r) rb = 0x7fc00000u;
+        h += mix64(((uint64_t)ux << 32) | rb);
+    }
+    __shared__ uint64_t red[256];
+    red[threadIdx.x] = h;
+    __syncthreads();
+    for (int s = 128; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) red[threadIdx.x] += red[threadIdx.x + s];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = red[0];
+    (void)nhi;
+}
+
+}  // namespace
+
+// ===========================================================================
+// C ABI
+// ===========================================================================
+struct lal_gpu_ctx {
+    int device;
+    int max_batch;
+    int max_vocab;
+};
+
+static thread_local hipError_t g_last_hip = hipSuccess;
+
+static int hip_fail(hipError_t e)
+{
+    g_last_hip = e;
+    return LAL_GPU_E_HIP;
+}
+
+#define LAL_HIP(call)                                  \
+    do {                                               \
+        hipError_t e_ = (call);                        \
+        if (e_ != hipSuccess) return hip_fail(e_);     \
+    } while (0)
+
+extern "C" {
+
+int lal_gpu_abi_version(void) { return LAL_GPU_ABI_VERSION; }
+
+int lal_gpu_last_hip_error(void) { return (int)g_last_hip; }
+
+const char *lal_gpu_strerror(int code)
+{
+    switch (code) {
+    case LAL_GPU_OK: return "ok";
+    case LAL_GPU_E_INVAL: return "invalid argument";
+    case LAL_GPU_E_RANGE: return "size above a context or library limit";
+    case LAL_GPU_E_HIP: return hipGetErrorString(g_last_hip);
+    case LAL_GPU_E_NOMEM: return "out of device memory";
+    case LAL_GPU_E_NODEV: return "no such device";
+    default: return "unknown error";
+    }
+}
+
+int lal_gpu_device_count(int *count)
+{
+    if (!count) return LAL_GPU_E_INVAL;
+    LAL_HIP(hipGetDeviceCount(count));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_set_device(int device)
+{
+    LAL_HIP(hipSetDevice(device));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
+{
+    if (!out || max_batch <= 0 || max_vocab <= 0) return LAL_GPU_E_INVAL;
+    *out = nullptr;
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess || device < 0 || device >= n) return LAL_GPU_E_NODEV;
+    LAL_HIP(hipSetDevice(device));
+    lal_gpu_ctx *c = (lal_gpu_ctx *)calloc(1, sizeof(lal_gpu_ctx));
+    if (!c) return LAL_GPU_E_NOMEM;
+    c->device = device;
+    c->max_batch = max_batch;
+    c->max_vocab = max_vocab;
+    *out = c;
+    return LAL_GPU_OK;
+}
+
+void lal_gpu_destroy(lal_gpu_ctx *ctx) { free(ctx); }
+
+int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_params *p,
+                   const lal_gpu_sample_io *io, void *stream)
+{
+    if (!ctx || !p || !io) return LAL_GPU_E_INVAL;
+    if (batch <= 0 || vocab <= 0) return LAL_GPU_E_INVAL;
+    if (batch > ctx->max_batch || vocab > ctx->max_vocab) return LAL_GPU_E_RANGE;
+    if (!io->logits || !io->out_token || io->ld < vocab) return LAL_GPU_E_INVAL;
+    const bool greedy = !(p->temperature > 0.0f) || p->top_k <= 0;
+    if (!greedy && p->top_k > LAL_GPU_MAX_K) return LAL_GPU_E_RANGE;
+    if (!greedy && !io->uniforms) return LAL_GPU_E_INVAL;
+    if (io->history && (io->history_ld <= 0 || io->history_ld > LAL_GPU_MAX_HISTORY))
+        return io->history_ld > LAL_GPU_MAX_HISTORY ? LAL_GPU_E_RANGE : LAL_GPU_E_INVAL;
+    if (io->allow_bits && io->allow_ld < (vocab + 31) / 32) return LAL_GPU_E_INVAL;
+    if (p->n_ban_ids < 0 || p->n_ban_ids > LAL_GPU_MAX_BAN_IDS) return LAL_GPU_E_RANGE;
+    if (p->n_ban_ids > 0 && !p->ban_ids) return LAL_GPU_E_INVAL;
+    if (p->variant != LAL_GPU_VARIANT_BASIC && p->variant != LAL_GPU_VARIANT_FILTERED)
+        return LAL_GPU_E_INVAL;
+    if (io->cand_ld < 0 || (io->cand_ld > 0 && !io->cand_ids && !io->cand_probs && !io->cand_kept))
+        return LAL_GPU_E_INVAL;
+    if (io->out_history_vals && !io->history) return LAL_GPU_E_INVAL;
+
+    KArgs A;
+    memset(&A, 0, sizeof A);
+    A.logits = io->logits;
+    A.logits_w = io->logits;
+    A.ld = io->ld;
+    A.V = vocab;
+    A.hist = io->history;
+    A.hist_ld = io->history ? io->history_ld : 0;
+    A.hist_len = io->history ? io->history_len : nullptr;
+    A.allow = io->allow_bits;
+    A.allow_ld = io->allow_ld;
+    A.bias = io->bias;
+    A.uniforms = io->uniforms;
+    A.out_token = io->out_token;
+    A.out_thr = io->out_threshold;
+    A.out_ncand = io->out_n_cand;
+    A.out_nkept = io->out_n_kept;
+    A.out_sum = io->out_sum;
+    A.cand_ld = io->cand_ld;
+    A.cand_ids = io->cand_ids;
+    A.cand_probs = io->cand_probs;
+    A.cand_kept = io->cand_kept;
+    A.out_hvals = io->out_history_vals;
+    A.ban_ids = p->ban_ids;
+    A.n_ban = p->n_ban_ids;
+    A.T = p->temperature;
+    A.top_p = p->top_p;
+    A.pen = p->rep_penalty;
+    A.k = p->top_k;
+    A.variant = p->variant;
+    A.flags = p->flags;
+    A.ban_last = p->ban_last;
+    A.ban_repeat = p->ban_repeat;
+    A.mask_recent = p->mask_recent;
+    A.greedy = greedy ? 1 : 0;
+    const bool has_hist = io->history != nullptr;
+    A.apply_pen = (p->rep_penalty > 1.0f && has_hist &&
+                   (p->variant == LAL_GPU_VARIANT_FILTERED || !greedy)) ? 1 : 0;
+    A.any_bans = (!greedy && ((has_hist && (p->ban_last || p->ban_repeat > 0)) || p->n_ban_ids > 0)) ? 1 : 0;
+    if (!has_hist) {
+        A.ban_last = 0;
+        A.ban_repeat = 0;
+        A.mask_recent = 0;
+    }
+    if (!A.any_bans) {
+        A.ban_last = 0;
+        A.ban_repeat = 0;
+        A.n_ban = 0;
+    }
+
+    hipStream_t s = (hipStream_t)stream;
+    const dim3 grid(batch), block(WG);
+    if (A.bias && A.allow)
+        hipLaunchKernelGGL((sample_rows_kernel<true, true>), grid, block, 0, s, A);
+    else if (A.bias)
+        hipLaunchKernelGGL((sample_rows_kernel<true, false>), grid, block, 0, s, A);
+    else if (A.allow)
+        hipLaunchKernelGGL((sample_rows_kernel<false, true>), grid, block, 0, s, A);
+    else
+        hipLaunchKernelGGL((sample_rows_kernel<false, false>), grid, block, 0, s, A);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_quantize_x(lal_gpu_ctx *ctx, const float *d_x, int batch, int n, int mode, int8_t *d_xq,
+                       float *d_sx, void *stream)
+{
+    if (!ctx || !d_x || !d_xq || !d_sx || batch <= 0 || n <= 0 || (mode != 0 && mode != 1))
+        return LAL_GPU_E_INVAL;
+    hipLaunchKernelGGL(quantize_x_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, d_x, n,
+                       mode, d_xq, d_sx);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_lm_head_q8(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx, int batch, int n,
+                       const int8_t *d_w, const float *d_sw, int vocab, float *d_logits, int ld,
+                       void *stream)
+{
+    if (!ctx || !d_xq || !d_sx || !d_w || !d_sw || !d_logits) return LAL_GPU_E_INVAL;
+    if (batch <= 0 || n <= 0 || vocab <= 0 || ld < vocab) return LAL_GPU_E_INVAL;
+    hipStream_t s = (hipStream_t)stream;
+    if (((uintptr_t)d_xq & 15) || ((uintptr_t)d_w & 15) || (n & 15)) {
+        // rows not 16-byte aligned: byte-load kernel
+        hipLaunchKernelGGL(lm_head_scalar_kernel, dim3((vocab + 3) / 4), dim3(256), 0, s, d_xq, d_sx,
+                           n, d_w, d_sw, vocab, d_logits, ld, batch);
+        LAL_HIP(hipGetLastError());
+        return LAL_GPU_OK;
+    }
+    const int waves = (vocab + LMH_ROWS - 1) / LMH_ROWS;
+    const dim3 grid((waves + 3) / 4), block(256);
+    for (int b0 = 0; b0 < batch; b0 += LMH_MAXB) {
+        const int nb = std::min(LMH_MAXB, batch - b0);
+        switch (nb) {
+        case 1: hipLaunchKernelGGL(lm_head_dot4_kernel<1>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        case 2: hipLaunchKernelGGL(lm_head_dot4_kernel<2>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        case 3: hipLaunchKernelGGL(lm_head_dot4_kernel<3>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        case 4: hipLaunchKernelGGL(lm_head_dot4_kernel<4>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        case 5: hipLaunchKernelGGL(lm_head_dot4_kernel<5>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        case 6: hipLaunchKernelGGL(lm_head_dot4_kernel<6>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        case 7: hipLaunchKernelGGL(lm_head_dot4_kernel<7>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        default: hipLaunchKernelGGL(lm_head_dot4_kernel<8>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        }
+        LAL_HIP(hipGetLastError());
+    }
+    return LAL_GPU_OK;
+}
+
+void lal_gpu_uniforms_rand(unsigned seed, int n, float *out, int gpt2)
+{
+    srand(seed);
+    for (int i = 0; i < n; i++) {
+        if (gpt2) out[i] = (float)(rand() % 1000000) / 1000000.0f;
+        else out[i] = (float)rand() / (float)RAND_MAX;
+    }
+}
+
+int lal_gpu_malloc(void **d_ptr, size_t bytes)
+{
+    if (!d_ptr) return LAL_GPU_E_INVAL;
+    hipError_t e = hipMalloc(d_ptr, bytes ? bytes : 1);
+    if (e == hipErrorOutOfMemory) {
+        g_last_hip = e;
+        return LAL_GPU_E_NOMEM;
+    }
+    LAL_HIP(e);
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_free(void *d_ptr)
+{
+    LAL_HIP(hipFree(d_ptr));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_memcpy_h2d(void *d_dst, const void *h_src, size_t bytes, void *stream)
+{
+    LAL_HIP(hipMemcpyAsync(d_dst, h_src, bytes, hipMemcpyHostToDevice, (hipStream_t)stream));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_memcpy_d2h(void *h_dst, const void *d_src, size_t bytes, void *stream)
+{
+    LAL_HIP(hipMemcpyAsync(h_dst, d_src, bytes, hipMemcpyDeviceToHost, (hipStream_t)stream));
+    LAL_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_memcpy_d2d(void *d_dst, const void *d_src, size_t bytes, void *stream)
+{
+    LAL_HIP(hipMemcpyAsync(d_dst, d_src, bytes, hipMemcpyDeviceToDevice, (hipStream_t)stream));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_memset(void *d_dst, int value, size_t bytes, void *stream)
+{
+    LAL_HIP(hipMemsetAsync(d_dst, value, bytes, (hipStream_t)stream));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_stream_create(void **stream)
+{
+    if (!stream) return LAL_GPU_E_INVAL;
+    hipStream_t s;
+    LAL_HIP(hipStreamCreateWithFlags(&s, hipStreamNonBlocking));
+    *stream = (void *)s;
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_stream_destroy(void *stream)
+{
+    LAL_HIP(hipStreamDestroy((hipStream_t)stream));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_stream_sync(void *stream)
+{
+    LAL_HIP(hipStreamSynchronize((hipStream_t)stream));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_device_sync(void)
+{
+    LAL_HIP(hipDeviceSynchronize());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_event_create(void **event)
+{
+    if (!event) return LAL_GPU_E_INVAL;
+    hipEvent_t e;
+    LAL_HIP(hipEventCreate(&e));
+    *event = (void *)e;
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_event_destroy(void *event)
+{
+    LAL_HIP(hipEventDestroy((hipEvent_t)event));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_event_record(void *event, void *stream)
+{
+    LAL_HIP(hipEventRecord((hipEvent_t)event, (hipStream_t)stream));
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_event_elapsed_ms(float *ms, void *start, void *stop)
+{
+    if (!ms) return LAL_GPU_E_INVAL;
+    LAL_HIP(hipEventSynchronize((hipEvent_t)stop));
+    LAL_HIP(hipEventElapsedTime(ms, (hipEvent_t)start, (hipEvent_t)stop));
+    return LAL_GPU_OK;
+}
+
+// ---- synthetic workloads ---------------------------------------------------
+static dim3 grid_for(size_t n)
+{
+    size_t blocks = (n + 255) / 256;
+    if (blocks > 65535) blocks = 65535;
+    if (blocks < 1) blocks = 1;
+    return dim3((unsigned)blocks);
+}
+
+int lal_gpu_synth_gauss(float *d_out, int batch, int vocab, int ld, unsigned long long seed, float sigma,
+                        float offset_range, int n_outliers, float outlier_value, void *stream)
+{
+    if (!d_out || batch <= 0 || vocab <= 0 || ld < vocab || n_outliers < 0 || n_outliers > 256)
+        return LAL_GPU_E_INVAL;
+    const dim3 grid((vocab + 256 * 16 - 1) / (256 * 16), batch);
+    hipLaunchKernelGGL(synth_gauss_kernel, grid, dim3(256), 0, (hipStream_t)stream, d_out, vocab, ld,
+                       (uint64_t)seed, sigma, offset_range, n_outliers, outlier_value);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_synth_zipf(float *d_out, int batch, int vocab, int ld, unsigned long long seed, float slope,
+                       float noise, void *stream)
+{
+    if (!d_out || batch <= 0 || vocab <= 0 || ld < vocab) return LAL_GPU_E_INVAL;
+    const dim3 grid((vocab + 256 * 16 - 1) / (256 * 16), batch);
+    hipLaunchKernelGGL(synth_zipf_kernel, grid, dim3(256), 0, (hipStream_t)stream, d_out, vocab, ld,
+                       (uint64_t)seed, slope, noise);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_synth_bits(uint32_t *d_out, int batch, int vocab, int words_ld, unsigned long long seed,
+                       float p_one, void *stream)
+{
+    if (!d_out || batch <= 0 || vocab <= 0 || words_ld < (vocab + 31) / 32) return LAL_GPU_E_INVAL;
+    const dim3 grid((words_ld + 255) / 256, batch);
+    hipLaunchKernelGGL(synth_bits_kernel, grid, dim3(256), 0, (hipStream_t)stream, d_out, vocab,
+                       words_ld, (uint64_t)seed, p_one);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_synth_int8(int8_t *d_out, size_t n, unsigned long long seed, int lo, int hi, void *stream)
+{
+    if (!d_out || lo > hi || lo < -128 || hi > 127) return LAL_GPU_E_INVAL;
+    hipLaunchKernelGGL(synth_int8_kernel, grid_for(n), dim3(256), 0, (hipStream_t)stream, d_out, n,
+                       (uint64_t)seed, lo, hi);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_synth_uniform(float *d_out, size_t n, unsigned long long seed, float lo, float hi, void *stream)
+{
+    if (!d_out) return LAL_GPU_E_INVAL;
+    hipLaunchKernelGGL(synth_uniform_kernel, grid_for(n), dim3(256), 0, (hipStream_t)stream, d_out, n,
+                       (uint64_t)seed, lo, hi);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_synth_normal(float *d_out, size_t n, unsigned long long seed, float sigma, void *stream)
+{
+    if (!d_out) return LAL_GPU_E_INVAL;
+    hipLaunchKernelGGL(synth_normal_kernel, grid_for(n), dim3(256), 0, (hipStream_t)stream, d_out, n,
+                       (uint64_t)seed, sigma);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_synth_ids(int *d_out, size_t n, unsigned long long seed, int vocab, void *stream)
+{
+    if (!d_out || vocab <= 0) return LAL_GPU_E_INVAL;
+    hipLaunchKernelGGL(synth_ids_kernel, grid_for(n), dim3(256), 0, (hipStream_t)stream, d_out, n,
+                       (uint64_t)seed, vocab);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+// Test hook: order-insensitive hash of glibc-restated expf over the inputs
+// [hi<<16, (hi+1)<<16) for hi in [first_hi, first_hi+nhi), one uint64 each.
+int lal_gpu_expf_check(unsigned first_hi, int nhi, unsigned long long *d_out, void *stream)
+{
+    if (!d_out || nhi <= 0 || first_hi + (unsigned)nhi > 65536u) return LAL_GPU_E_INVAL;
+    hipLaunchKernelGGL(expf_check_kernel, dim3(nhi), dim3(256), 0, (hipStream_t)stream, first_hi, nhi,
+                       (uint64_t *)d_out);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+}  // extern "C"

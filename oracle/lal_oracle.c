@@ -156,6 +156,16 @@ int lal_oracle_sample_row(float *row, int V, const lal_oracle_params *p,
         for (int v = 0; v < V; v++) n += (y[v] >= inf.threshold);
         inf.n_cand = n;
         inf.n_kept = 1;
+        if (cand_ids || cand_probs || cand_kept) {
+            int i = 0;
+            for (int v = 0; v < V && i < cand_cap; v++) {
+                if (!(y[v] >= inf.threshold)) continue;
+                if (cand_ids) cand_ids[i] = v;
+                if (cand_kept) cand_kept[i] = (unsigned char)(v == token);
+                if (cand_probs) cand_probs[i] = (v == token) ? 1.0f : 0.0f;
+                i++;
+            }
+        }
         if (info) *info = inf;
         free(y);
         return token;
@@ -430,6 +440,38 @@ int lal_oracle_filter_norepeat6(int *keep_mask, int n_vocab, int last_token,
 {
     (void)decode_fn;
     return ban_recent(keep_mask, n_vocab, last_token, recent, n_recent, 6);
+}
+
+/* Per-chunk hash of glibc expf over every float input x = (hi<<16)|lo,
+ * lo in [0, 65536): out[i] for hi = first_hi + i.  The GPU's expf
+ * restatement is checked against these sums (same mixing function). */
+static uint64_t mix64(uint64_t z)
+{
+    z += 0x9E3779B97F4A7C15ull;
+    z = (z ^ (z >> 30)) * 0xBF58476D1CE4E5B9ull;
+    z = (z ^ (z >> 27)) * 0x94D049BB133111EBull;
+    return z ^ (z >> 31);
+}
+
+void lal_oracle_expf_checksums(unsigned first_hi, int nhi, uint64_t *out)
+{
+#ifdef _OPENMP
+#pragma omp parallel for schedule(dynamic, 16)
+#endif
+    for (int i = 0; i < nhi; i++) {
+        uint64_t h = 0;
+        uint32_t hi = first_hi + (uint32_t)i;
+        for (uint32_t lo = 0; lo < 65536u; lo++) {
+            uint32_t ux = (hi << 16) | lo, rb;
+            float x, r;
+            memcpy(&x, &ux, 4);
+            r = expf(x);
+            memcpy(&rb, &r, 4);
+            if (r != r) rb = 0x7fc00000u;
+            h += mix64(((uint64_t)ux << 32) | rb);
+        }
+        out[i] = h;
+    }
 }
 
 /* lal_sampling.h:133-136: append, or drop the oldest once 256 are held */

@@ -124,6 +124,10 @@ int lal_oracle_filter_norepeat6(int *keep_mask, int n_vocab, int last_token,
                                 const int *recent, int n_recent,
                                 lal_oracle_decode_fn decode_fn);
 
+/* Hash of glibc expf over all inputs with high half-word in
+ * [first_hi, first_hi+nhi): see lal_gpu_expf_check. */
+void lal_oracle_expf_checksums(unsigned first_hi, int nhi, uint64_t *out);
+
 /* Exact k-th largest (with multiplicity) by brute-force sort: a pin for the
  * heap selection that does not share its code. */
 float lal_oracle_kth_largest_sorted(const float *x, int n, int k);

@@ -76,6 +76,7 @@ class Oracle:
         L.lal_oracle_kth_largest_sorted.restype = C.c_float
         L.lal_oracle_kth_largest_sorted.argtypes = [_fp, C.c_int, C.c_int]
         L.lal_oracle_recent_push.argtypes = [C.c_void_p, C.c_int]
+        L.lal_oracle_expf_checksums.argtypes = [C.c_uint, C.c_int, C.POINTER(C.c_uint64)]
         self.filter_antirepeat4 = C.cast(L.lal_oracle_filter_antirepeat4, C.c_void_p).value
         self.filter_norepeat6 = C.cast(L.lal_oracle_filter_norepeat6, C.c_void_p).value
         self.filter_fn = {"antirepeat4": self.filter_antirepeat4,
@@ -147,6 +148,11 @@ class Oracle:
         s = np.zeros(V, np.float32)
         self.L.lal_oracle_quantize_w(_ptr(W, _fp), _ptr(q, C.POINTER(C.c_int8)), _ptr(s, _fp), n, V)
         return q, s
+
+    def expf_checksums(self, first_hi, nhi):
+        out = np.zeros(nhi, np.uint64)
+        self.L.lal_oracle_expf_checksums(first_hi, nhi, out.ctypes.data_as(C.POINTER(C.c_uint64)))
+        return out
 
     def expf(self, x):
         return np.float32(self.L.lal_oracle_expf(C.c_float(x)))

@@ -1,0 +1,237 @@
+"""GPU parity of the HIP sampler (through the C ABI) against the reference's
+golden vectors and the CPU oracle on identical bytes.
+
+Bar: token ids, thresholds, pool sizes, pool membership and the in-place
+penalised logits bit-exact; probabilities within 1e-5 relative (fp32)."""
+import numpy as np
+import pytest
+
+import golden_cases
+import synth
+from gpu_helpers import GpuRun, assert_same, log, oracle_run
+from oracle_lib import Oracle
+
+pytestmark = pytest.mark.gpu
+
+V7B = 152064
+VGPT2 = 50257
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from lal_amd import abi
+    d = abi.Device(0, max_batch=1024, max_vocab=V7B)
+    yield d
+    d.close()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return Oracle()
+
+
+@pytest.fixture(scope="module")
+def run(dev):
+    return GpuRun(dev)
+
+
+def synth_dev(dev, fn, *args):
+    from lal_amd import abi
+    abi.check(getattr(dev.lib, fn)(*args), fn)
+
+
+def gpu_logits(dev, kind, B, V, ld, seed, **kw):
+    """Generate a [B][ld] logit batch on the GPU and return it on the host."""
+    import ctypes as C
+    from lal_amd import abi
+    buf = dev.alloc(4 * B * ld)
+    if kind == "gauss":
+        synth_dev(dev, "lal_gpu_synth_gauss", abi.ptr(buf), B, V, ld, seed, C.c_float(kw.get("sigma", 2.5)),
+                  C.c_float(kw.get("offset", 0.0)), kw.get("outliers", 0), C.c_float(12.0), dev.stream)
+    else:
+        synth_dev(dev, "lal_gpu_synth_zipf", abi.ptr(buf), B, V, ld, seed, C.c_float(1.1),
+                  C.c_float(0.3), dev.stream)
+    dev.sync()
+    out = buf.download((B, ld), np.float32)
+    buf.close()
+    if ld > V:
+        out[:, V:] = np.nan
+    return out
+
+
+# ---------------------------------------------------------------------------
+# golden vectors from the reference's own C code
+# ---------------------------------------------------------------------------
+def test_golden_reference_cases(dev, run):
+    from lal_amd import abi
+    G = golden_cases.load()
+    for spec in G["sampler"]:
+        log(f"golden case {spec['id']} {spec['variant']} {spec['kind']} V={spec['V']} k={spec['k']}")
+        row, h = golden_cases.inputs(spec)
+        u = np.array([golden_cases.f32(spec["u_bits"])], np.float32)
+        variant = abi.VARIANT_FILTERED if spec["variant"] == "filtered" else abi.VARIANT_BASIC
+        bans = {}
+        if spec["filter"] == "antirepeat4":
+            bans = dict(ban_last=1, ban_repeat=4)
+        elif spec["filter"] == "norepeat6":
+            bans = dict(ban_last=1, ban_repeat=6)
+        res = run(row[None, :], T=spec["T"], k=spec["k"], pen=spec["pen"], variant=variant,
+                  flags=abi.F_WRITEBACK, hist=None if h is None else h[None, :], u=u,
+                  want_hvals=True, **bans)
+        assert int(res["token"][0]) == spec["token"], f"case {spec['id']}: gpu {res['token'][0]} ref {spec['token']}"
+        assert synth.digest(res["logits_after"][0]) == spec["out_digest"], f"case {spec['id']}: in-place penalty"
+        if h is not None:
+            for i, b in enumerate(spec["hist_after_bits"]):
+                if b is not None:
+                    assert res["hvals"][0, i].view(np.uint32) == b, f"case {spec['id']} hist {i}"
+
+
+# ---------------------------------------------------------------------------
+# the measured workloads at full size, against the oracle on the same bytes
+# ---------------------------------------------------------------------------
+def test_qwen7b_single_stream(dev, run, orc):
+    """1 x 152064, N(0, 2.5^2) + 8 outliers at +12, penalty 1.1 over 64 ids, T 0.7, k 40."""
+    x = gpu_logits(dev, "gauss", 1, V7B, V7B, 11, outliers=8)
+    hist = synth.history(3, 1, 64, V7B)
+    for seed in range(8):
+        u = orc.uniforms(seed, 1)
+        kw = dict(T=0.7, k=40, pen=1.1, hist=hist, u=u, cand_ld=64)
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=64)
+
+
+def test_gpt2_batched_unaligned_rows(dev, run, orc):
+    """256 x 50257 with ld = 50257 (rows not 16-byte aligned), penalty 1.2 over 128 ids."""
+    B = 256
+    x = gpu_logits(dev, "gauss", B, VGPT2, VGPT2, 12, sigma=3.0, offset=5.0)
+    hist = synth.history(4, B, 128, VGPT2)
+    u = orc.uniforms(42, B)
+    kw = dict(T=1.0, k=40, pen=1.2, hist=hist, u=u, cand_ld=64)
+    assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=64)
+
+
+def test_qwen7b_batched_topk_topp(dev, run, orc):
+    """1024 x 152064 Zipf rows, penalty 1.1 over 256 ids, T 0.8, top-k 50, top-p 0.9."""
+    B = 1024
+    x = gpu_logits(dev, "zipf", B, V7B, V7B, 13)
+    hist = synth.history(5, B, 256, V7B)
+    u = orc.uniforms(7, B)
+    kw = dict(T=0.8, k=50, top_p=0.9, pen=1.1, hist=hist, u=u, cand_ld=64)
+    g = run(x, **kw)
+    o = oracle_run(orc, x, **kw)
+    assert_same(g, o, cand_ld=64)
+    assert np.all(g["n_kept"] <= g["n_cand"]) and np.all(g["n_cand"] >= 50)
+
+
+def test_constrained_decoding(dev, run, orc):
+    """512 x 152064, 5% allow mask, shared sparse bias (2000 nnz), last 16 ids -inf, T 0.7, k 40."""
+    import ctypes as C
+    from lal_amd import abi
+    B = 512
+    x = gpu_logits(dev, "gauss", B, V7B, V7B, 14)
+    words = (V7B + 31) // 32
+    buf = dev.alloc(4 * B * words)
+    synth_dev(dev, "lal_gpu_synth_bits", abi.ptr(buf), B, V7B, words, 99, C.c_float(0.05), dev.stream)
+    dev.sync()
+    allow = buf.download((B, words), np.uint32)
+    buf.close()
+    bias = synth.sparse_bias(15, V7B, 2000, 1.5)
+    hist = synth.history(6, B, 16, V7B)
+    u = orc.uniforms(8, B)
+    kw = dict(T=0.7, k=40, pen=1.0, hist=hist, allow=allow, bias=bias, mask_recent=16, u=u,
+              cand_ld=64)
+    g = run(x, **kw)
+    o = oracle_run(orc, x, **kw)
+    assert_same(g, o, cand_ld=64)
+    # every sampled token is allowed and not among the last 16 ids
+    for b in range(B):
+        t = int(g["token"][b])
+        assert (allow[b, t >> 5] >> (t & 31)) & 1
+        assert t not in set(hist[b].tolist())
+
+
+# ---------------------------------------------------------------------------
+# variants and edge cases
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("variant", [0, 1])
+@pytest.mark.parametrize("kind", ["gauss", "ties", "neginf", "ascending", "const", "allneginf",
+                                  "signed_zero", "huge", "zipf"])
+def test_row_kinds(run, orc, variant, kind):
+    B, V = 6, 20011
+    x = np.stack([synth.make_row(kind, 31 * b + 1, V) for b in range(B)])
+    hist = synth.history(9, B, 32, V, with_invalid=True)
+    u = np.array([0.0, 1.0, 0.5, 0.25, 0.999, 1e-7], np.float32)
+    for k in (1, 7, 40, 512):
+        kw = dict(T=0.9, k=k, pen=1.15, variant=variant, hist=hist, u=u, cand_ld=600)
+        log(f"kinds {kind} variant {variant} k {k}")
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=600)
+
+
+@pytest.mark.parametrize("top_p", [1e-6, 0.3, 0.9, 0.999999, 1.0])
+@pytest.mark.parametrize("kind", ["gauss", "ties", "zipf", "outliers"])
+def test_top_p(run, orc, top_p, kind):
+    B, V = 8, 30000
+    x = np.stack([synth.make_row(kind, 7 * b + 3, V) for b in range(B)])
+    hist = synth.history(10, B, 64, V)
+    u = synth.uniform(5, 0, B)
+    for k in (1, 5, 50, 300):
+        kw = dict(T=0.8, k=k, top_p=top_p, pen=1.1, hist=hist, u=u, cand_ld=512)
+        log(f"top_p {top_p} {kind} k {k}")
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=512)
+
+
+def test_bans_and_gpt2_draw(run, orc):
+    from lal_amd import abi
+    B, V = 16, 4099
+    x = np.stack([synth.make_row("descending" if b % 2 else "gauss", b, V) for b in range(B)])
+    hist = synth.history(11, B, 12, V)
+    hist[:, -1] = 0          # ban_last hits the top token of descending rows
+    hist[:, -2] = 1
+    u = synth.uniform(6, 0, B)
+    u[0] = 0.0
+    for variant in (0, 1):
+        for bl, br, ids in ((1, 0, None), (0, 4, None), (1, 6, [2, 3, 5, 4098]),
+                            (0, 0, list(range(0, 60)))):
+            for flags in (0, abi.F_DRAW_GPT2):
+                kw = dict(T=0.8, k=3, pen=1.1, variant=variant, flags=flags, hist=hist, u=u,
+                          ban_last=bl, ban_repeat=br, ban_ids=ids, cand_ld=64)
+                log(f"bans variant {variant} {bl} {br} {ids is not None} flags {flags}")
+                assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=64)
+
+
+def test_greedy_and_small_vocab(run, orc):
+    for V in (1, 2, 3, 5, 17, 64, 8191, 8192, 8193, 16387):
+        x = np.stack([synth.make_row(k, V, V) for k in ("gauss", "ties", "const", "allneginf")])
+        hist = synth.history(12, 4, 8, V)
+        for T, k in ((0.0, 40), (0.7, 0), (0.7, 1), (0.7, 3), (1.3, 512)):
+            for variant in (0, 1):
+                kw = dict(T=T, k=k, pen=1.2, variant=variant, hist=hist,
+                          u=np.array([0.1, 0.5, 0.9, 0.0], np.float32), cand_ld=8)
+                log(f"small V={V} T={T} k={k} variant={variant}")
+                assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=8)
+
+
+def test_history_len_and_ld(run, orc):
+    B, V, ld = 9, 12345, 12352
+    x = np.full((B, ld), np.nan, np.float32)
+    x[:, :V] = np.stack([synth.make_row("gauss", 100 + b, V) for b in range(B)])
+    hist = synth.history(13, B, 40, V)
+    hl = np.array([0, 1, 2, 5, 17, 39, 40, 3, 0], np.int32)
+    u = synth.uniform(9, 0, B)
+    for variant in (0, 1):
+        kw = dict(V=V, T=0.9, k=20, pen=1.3, variant=variant, hist=hist, hist_len=hl, u=u,
+                  ban_last=1, ban_repeat=3, mask_recent=2, cand_ld=64)
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=64)
+
+
+def test_expf_matches_glibc_exhaustively(dev, orc):
+    """The GPU expf restatement equals glibc expf on all 2^32 float inputs."""
+    from lal_amd import abi
+    n = 65536
+    buf = dev.alloc(8 * n)
+    abi.check(dev.lib.lal_gpu_expf_check(0, n, abi.ptr(buf), dev.stream), "expf_check")
+    dev.sync()
+    g = buf.download(n, np.uint64)
+    buf.close()
+    c = orc.expf_checksums(0, n)
+    bad = np.nonzero(g != c)[0]
+    assert len(bad) == 0, f"expf differs from glibc in chunks {bad[:10]} (inputs hi<<16)"
