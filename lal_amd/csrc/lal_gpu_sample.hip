@@ -520,44 +520,6 @@ __device__ float rescan_value(const KArgs &A, const Smem &S, const float *row, c
     return exact_value(S, use_hash, e, yh);
 }
 
-// Fills S.ep[0..n) for the element chunk starting at `e0` (n consecutive ids
-// handled as: thread tid owns ids e0+4tid .. e0+4tid+3 for float4 chunks, or
-// e0+tid for scalar chunks) with kept ? e : -1.
-template <bool HAS_BIAS, bool HAS_ALLOW>
-__device__ void rescan_chunk_e(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
-                               bool use_hash, float T, bool use_keep_ban, float mx, int e_begin,
-                               int n, bool vec)
-{
-    __syncthreads();
-    if (vec) {
-        const int base = 4 * threadIdx.x;
-        if (base < n) {
-            const float4 xv = *reinterpret_cast<const float4 *>(row + e_begin + base);
-            const float xs[4] = {xv.x, xv.y, xv.z, xv.w};
-#pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                const int e = e_begin + base + c;
-                const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, xs[c]);
-                bool kept = (yv >= T);
-                if (kept && use_keep_ban) {
-                    const int s = hash_find(S, e);
-                    if (s >= 0 && (S.hinfo[s] & HF_BAN)) kept = false;
-                }
-                S.ep[base + c] = kept ? glibc_expf((yv - mx) / A.T) : -1.0f;
-            }
-        }
-    } else if ((int)threadIdx.x < n) {
-        const int e = e_begin + threadIdx.x;
-        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
-        bool kept = (yv >= T);
-        if (kept && use_keep_ban) {
-            const int s = hash_find(S, e);
-            if (s >= 0 && (S.hinfo[s] & HF_BAN)) kept = false;
-        }
-        S.ep[threadIdx.x] = kept ? glibc_expf((yv - mx) / A.T) : -1.0f;
-    }
-}
-
 struct RescanStats {
     int n_cand, n_kept;
     float max_kept;     // max over the set, plain max (no -1e30 floor)
@@ -604,51 +566,111 @@ __device__ RescanStats rescan_stats(const KArgs &A, Smem &S, const float *row, c
 }
 
 // Sequential sum (draw == false) or draw (draw == true) over the row in id
-// order.  Returns the sum, or via *token the first kept id with r <= acc.
+// order, 1024 ids at a time.  Returns the sum; with draw, *token receives the
+// first kept id whose running sum reaches r (-1 when none does).
+constexpr int RS_CHUNK = 1024;
+static_assert(RS_CHUNK <= CAP, "rescan chunk lives in S.ep");
+
 template <bool HAS_BIAS, bool HAS_ALLOW>
 __device__ float rescan_sequential(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
-                                   const RowGeo &g, bool use_hash, float T, bool use_ban, float mx,
-                                   bool draw, float r, int *token)
+                                   bool use_hash, float T, bool use_ban, float mx, bool draw,
+                                   float r, int *token)
 {
     float acc = 0.0f;
     int found = -1;
-    // chunk list in id order: head, body float4 chunks (1024 ids each), tail
-    auto run = [&](int e_begin, int n, bool vec) {
-        if (n <= 0) return;
-        rescan_chunk_e<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, mx, e_begin, n, vec);
+    for (int c0 = 0; c0 < A.V; c0 += RS_CHUNK) {
+        const int n = min(RS_CHUNK, A.V - c0);
+        bool kept[RS_CHUNK / WG];
         __syncthreads();
-        if (wave_id() == 0 && found < 0) {
-            for (int base = 0; base < n && found < 0; base += 64) {
-                const int i = base + lane_id();
-                const float e = (i < n) ? S.ep[i] : -1.0f;
-                if (!__ballot(!(e < 0.0f))) continue;
-                const int ebits = __float_as_int(e);
-                const int lim = min(64, n - base);
-                for (int l = 0; l < lim; ++l) {
-                    const float el = __int_as_float(__builtin_amdgcn_readlane(ebits, l));
-                    if (el < 0.0f) continue;
-                    acc = acc + el;
-                    if (draw && r <= acc) { found = e_begin + base + l; break; }
+#pragma unroll
+        for (int q = 0; q < RS_CHUNK / WG; ++q) {
+            const int i = (int)threadIdx.x + q * WG;
+            kept[q] = false;
+            if (i < n) {
+                const int e = c0 + i;
+                const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
+                kept[q] = (yv >= T);
+                if (kept[q] && use_ban) {
+                    const int s = hash_find(S, e);
+                    if (s >= 0 && (S.hinfo[s] & HF_BAN)) kept[q] = false;
+                }
+                S.ep[i] = kept[q] ? glibc_expf((yv - mx) / A.T) : -1.0f;
+            }
+        }
+        acc = block_seq_prefix(S, n, acc);
+        if (draw) {
+            int first = INT_MAX;
+#pragma unroll
+            for (int q = 0; q < RS_CHUNK / WG; ++q) {
+                const int i = (int)threadIdx.x + q * WG;
+                if (i < n && kept[q] && r <= S.ep[i]) first = min(first, i);
+            }
+            first = block_min(S, first);
+            if (first != INT_MAX) {
+                found = c0 + first;
+                break;
+            }
+        }
+    }
+    if (token) *token = found;
+    return acc;
+}
+
+// Candidate outputs for a rescanned row: the first cand_ld pool ids in id
+// order with their kept flag and probability e/sum.
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__device__ void rescan_write_cands(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
+                                   bool use_hash, float T, bool use_ban, float mx, float sum,
+                                   bool greedy, int greedy_token, int b)
+{
+    int written = 0;
+    for (int c0 = 0; c0 < A.V && written < A.cand_ld; c0 += RS_CHUNK) {
+        const int n = min(RS_CHUNK, A.V - c0);
+        int e_of[RS_CHUNK / WG];
+        float y_of[RS_CHUNK / WG];
+        int mine = 0;
+#pragma unroll
+        for (int q = 0; q < RS_CHUNK / WG; ++q) {
+            const int i = (int)threadIdx.x * (RS_CHUNK / WG) + q;  // contiguous ids per thread
+            e_of[q] = -1;
+            if (i < n) {
+                const int e = c0 + i;
+                y_of[q] = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
+                if (y_of[q] >= T) {
+                    e_of[q] = e;
+                    mine++;
                 }
             }
         }
-        if (wave_id() == 0 && lane_id() == 0) S.bcast = found;
+        int tot;
+        int pos = written + block_excl_scan(mine, tot, S.wsum[(c0 / RS_CHUNK) & 1]);
+#pragma unroll
+        for (int q = 0; q < RS_CHUNK / WG; ++q) {
+            if (e_of[q] < 0) continue;
+            if (pos < A.cand_ld) {
+                const int e = e_of[q];
+                bool kept;
+                if (greedy) {
+                    kept = (e == greedy_token);
+                } else {
+                    kept = true;
+                    if (use_ban) {
+                        const int s = hash_find(S, e);
+                        if (s >= 0 && (S.hinfo[s] & HF_BAN)) kept = false;
+                    }
+                }
+                const size_t o = (size_t)b * A.cand_ld + pos;
+                if (A.cand_ids) A.cand_ids[o] = e;
+                if (A.cand_kept) A.cand_kept[o] = kept ? 1 : 0;
+                if (A.cand_probs)
+                    A.cand_probs[o] = greedy ? (kept ? 1.0f : 0.0f)
+                                             : (kept ? glibc_expf((y_of[q] - mx) / A.T) / sum : 0.0f);
+            }
+            pos++;
+        }
+        written += tot;
         __syncthreads();
-        found = S.bcast;
-    };
-    run(0, g.head, false);
-    for (int t = 0; t < (g.nb4 + WG - 1) / WG && found < 0; ++t) {
-        const int q0 = t * WG;
-        const int nq = min(WG, g.nb4 - q0);
-        run(g.head + 4 * q0, 4 * nq, true);
     }
-    if (found < 0) run(g.tail0, g.ntail, false);
-    if (wave_id() == 0 && lane_id() == 0) S.redf[0] = acc;
-    __syncthreads();
-    const float tot = S.redf[0];
-    __syncthreads();
-    if (token) *token = found;
-    return tot;
 }
 
 // ---------------------------------------------------------------------------
@@ -923,23 +945,18 @@ __global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
                 for (int r = 0; r < PER; ++r)
                     if (prk[r] >= 0) S.ep[prk[r]] = pr[r];
                 __syncthreads();
-                // inclusive cumulative cutoff in sorted order
-                if (wave_id() == 0) {
-                    float cum = 0.0f;
-                    int cut = -1;
-                    for (int base = 0; base < nc && cut < 0; base += 64) {
-                        const int i = base + lane_id();
-                        const int pb = __float_as_int((i < nc) ? S.ep[i] : 0.0f);
-                        const int lim = min(64, nc - base);
-                        for (int l = 0; l < lim; ++l) {
-                            cum = cum + __int_as_float(__builtin_amdgcn_readlane(pb, l));
-                            if (cum >= A.top_p) { cut = base + l; break; }
-                        }
-                    }
-                    if (lane_id() == 0) S.bcast = (cut < 0) ? nc - 1 : cut;
+                // inclusive cumulative cutoff in sorted order: the running
+                // sum is monotone, so the cut is the first sorted position
+                // whose prefix reaches top_p (none: keep the whole pool)
+                block_seq_prefix(S, nc, 0.0f);
+                int fc = INT_MAX;
+#pragma unroll
+                for (int r = 0; r < PER; ++r) {
+                    const int j = tid + r * WG;
+                    if (j < nc && S.ep[j] >= A.top_p) fc = min(fc, j);
                 }
-                __syncthreads();
-                const int cut = S.bcast;
+                fc = block_min(S, fc);
+                const int cut = (fc == INT_MAX) ? nc - 1 : fc;
 #pragma unroll
                 for (int r = 0; r < PER; ++r) nuc[r] = (prk[r] >= 0) && (prk[r] <= cut);
             }
@@ -1032,10 +1049,13 @@ __global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
             if (A.greedy) {
                 token = st.first_kept;
                 n_kept = 1;
+                if (A.cand_ld > 0)
+                    rescan_write_cands<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false, 0.0f,
+                                                            1.0f, true, token, b);
             } else {
                 const float mx = (st.max_kept > -1e30f) ? st.max_kept : -1e30f;
-                sum2 = rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, use_hash, T,
-                                                              use_ban, mx, false, 0.0f, nullptr);
+                sum2 = rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban,
+                                                              mx, false, 0.0f, nullptr);
                 if (A.variant == LAL_GPU_VARIANT_FILTERED && sum2 <= 0.0f) {
                     token = (st.max_kept > -1e30f) ? st.first_max_kept : 0;
                 } else {
@@ -1044,11 +1064,14 @@ __global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
                         token = 0;
                     } else {
                         int f = -1;
-                        rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, use_hash, T,
-                                                               use_ban, mx, true, rr, &f);
+                        rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban,
+                                                               mx, true, rr, &f);
                         token = (f < 0) ? V - 1 : f;
                     }
                 }
+                if (A.cand_ld > 0)
+                    rescan_write_cands<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, mx,
+                                                            sum2, false, token, b);
             }
         }
     }

@@ -138,5 +138,7 @@ def assert_same(gpu, ora, cand_ld=0, check_probs=True, rows=None):
             assert np.array_equal(gpu["cand_kept"][b, :n], ora["cand_kept"][b, :n]), f"cand kept row {b}"
             if check_probs:
                 pg, po = gpu["cand_probs"][b, :n], ora["cand_probs"][b, :n]
-                rel = np.abs(pg - po) / np.maximum(np.abs(po), 1e-30)
-                assert np.all((rel <= 1e-5) | (po == pg)), f"probs row {b}: max rel {rel.max()}"
+                with np.errstate(invalid="ignore", divide="ignore"):
+                    rel = np.abs(pg - po) / np.maximum(np.abs(po), 1e-30)
+                ok = (pg == po) | (np.isnan(pg) & np.isnan(po)) | (rel <= 1e-5)
+                assert np.all(ok), f"probs row {b}: max rel {np.nanmax(rel)}"
