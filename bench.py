@@ -1,0 +1,254 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X token sampler (lal_amd/liblal_gpu.so, C ABI).
+
+Default workload: the batched Qwen2.5-7B-vocab sampling step -- 1024 rows of
+fp32 logits over a 152064 vocab, Zipf-shaped (-1.1 ln(rank) + N(0, 0.3^2)
+over a per-row permutation), repetition penalty 1.1 over 256 history ids per
+row, temperature 0.8, top-k 50, then top-p 0.9, one uniform per row from the
+reference RNG stream (srand(seed); (float)rand()/RAND_MAX).
+
+A step is one lal_gpu_sample call over the whole batch.  Inputs are resident
+in HBM before timing; two input sets (2 x 623 MB) alternate between steps so
+the 256 MB Infinity Cache cannot serve them.  Timing uses HIP events recorded
+on the stream the sampler runs on.  Prints one JSON line.
+"""
+import argparse
+import ctypes as C
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
+
+WORKLOADS = {
+    # name: (batch, vocab, kind, T, k, top_p, penalty, history, extra)
+    "qwen7b_batched_topk_topp": dict(B=1024, V=152064, kind="zipf", T=0.8, k=50, top_p=0.9,
+                                     pen=1.1, H=256),
+    "qwen7b_single_stream": dict(B=1, V=152064, kind="outliers", T=0.7, k=40, top_p=0.0,
+                                 pen=1.1, H=64),
+    "gpt2_batched": dict(B=256, V=50257, kind="gauss_offset", T=1.0, k=40, top_p=0.0, pen=1.2,
+                         H=128),
+    "constrained": dict(B=512, V=152064, kind="gauss", T=0.7, k=40, top_p=0.0, pen=1.0, H=16,
+                        allow=0.05, bias_nnz=2000, mask_recent=16),
+}
+
+
+def algorithmic_bytes_per_row(w):
+    """Compulsory HBM traffic per row: logits read once, history ids read
+    once, the uniform read and the token written; for the constrained
+    workload also the row's allow-mask words (the shared bias is per step)."""
+    b = 4 * w["V"] + 4 * w["H"] + 4 + 4
+    if w.get("allow"):
+        b += 4 * ((w["V"] + 31) // 32)
+    return b
+
+
+def algorithmic_bytes_per_step(w):
+    b = w["B"] * algorithmic_bytes_per_row(w)
+    if w.get("bias_nnz"):
+        b += 4 * w["V"]
+    return b
+
+
+class Inputs:
+    def __init__(self, dev, w, seed):
+        from lal_amd import abi
+        lib = dev.lib
+        B, V, H = w["B"], w["V"], w["H"]
+        self.logits = dev.alloc(4 * B * V)
+        if w["kind"] == "zipf":
+            abi.check(lib.lal_gpu_synth_zipf(abi.ptr(self.logits), B, V, V, seed, C.c_float(1.1),
+                                             C.c_float(0.3), dev.stream), "synth")
+        else:
+            sigma, off, nout = {"outliers": (2.5, 0.0, 8), "gauss_offset": (3.0, 5.0, 0),
+                                "gauss": (2.5, 0.0, 0)}[w["kind"]]
+            abi.check(lib.lal_gpu_synth_gauss(abi.ptr(self.logits), B, V, V, seed, C.c_float(sigma),
+                                              C.c_float(off), nout, C.c_float(12.0), dev.stream),
+                      "synth")
+        self.hist = dev.alloc(4 * B * H)
+        abi.check(lib.lal_gpu_synth_ids(abi.ptr(self.hist), B * H, seed + 1, V, dev.stream), "ids")
+        u = np.zeros(B, np.float32)
+        lib.lal_gpu_uniforms_rand(seed & 0xFFFFFFFF, B, u.ctypes.data_as(C.POINTER(C.c_float)), 0)
+        self.u = dev.put(u)
+        self.allow = None
+        self.words = (V + 31) // 32
+        if w.get("allow"):
+            self.allow = dev.alloc(4 * B * self.words)
+            abi.check(lib.lal_gpu_synth_bits(abi.ptr(self.allow), B, V, self.words, seed + 2,
+                                             C.c_float(w["allow"]), dev.stream), "bits")
+        self.bias = None
+        if w.get("bias_nnz"):
+            rng = np.random.default_rng(seed)
+            bias = np.zeros(V, np.float32)
+            idx = rng.choice(V, w["bias_nnz"], replace=False)
+            bias[idx] = (rng.standard_normal(w["bias_nnz"]) * 1.5).astype(np.float32)
+            self.bias = dev.put(bias)
+        self.tok = dev.alloc(4 * B)
+        dev.sync()
+
+    def io(self, w):
+        from lal_amd import abi
+        io = abi.SampleIO()
+        io.logits = self.logits.ptr
+        io.ld = w["V"]
+        io.history = self.hist.ptr
+        io.history_ld = w["H"]
+        io.uniforms = self.u.ptr
+        io.out_token = self.tok.ptr
+        if self.allow is not None:
+            io.allow_bits = self.allow.ptr
+            io.allow_ld = self.words
+        if self.bias is not None:
+            io.bias = self.bias.ptr
+        return io
+
+
+def params_for(w):
+    from lal_amd import abi
+    return abi.make_params(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"],
+                           variant=abi.VARIANT_BASIC, mask_recent=w.get("mask_recent", 0))
+
+
+def cpu_baseline(w, dev, inputs, target_s=4.0):
+    """The CPU oracle (C, OpenMP over rows) on the same bytes: a bounded
+    sample of the workload's rows, timed on this host's cores."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_lib import Oracle, make_params as oparams
+    orc = Oracle()
+    B, V, H = w["B"], w["V"], w["H"]
+    nrows = min(B, 256)
+    x = inputs.logits.download((B, V), np.float32)[:nrows].copy()
+    h = inputs.hist.download((B, H), np.int32)[:nrows].copy()
+    u = inputs.u.download(B, np.float32)[:nrows].copy()
+    allow = inputs.allow.download((B, inputs.words), np.uint32)[:nrows].copy() if inputs.allow is not None else None
+    bias = inputs.bias.download(V, np.float32) if inputs.bias is not None else None
+    p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"],
+                mask_recent=w.get("mask_recent", 0))
+    threads = os.cpu_count() or 1
+    try:
+        threads = len(os.sched_getaffinity(0))
+    except AttributeError:
+        pass
+    threads = int(os.environ.get("OMP_NUM_THREADS", threads))
+
+    def timed(nthreads, rows_target_s):
+        done, t0 = 0, time.perf_counter()
+        reps = 0
+        while True:
+            xx = x.copy()  # the sampler penalises in place
+            orc.sample_batch(xx, p, hist=h, allow=allow, bias=bias, uniforms=u, nthreads=nthreads)
+            done += nrows
+            reps += 1
+            el = time.perf_counter() - t0
+            if el >= rows_target_s or reps >= 64:
+                return done / el, done
+
+    rows_s, done = timed(threads, target_s)
+    rows_s1, done1 = timed(1, target_s / 4)
+    return {"value": rows_s, "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{done} rows (first {nrows} rows of the step's batch, repeated), "
+                      f"OpenMP over rows; 1-thread: {rows_s1:.1f} rows/s over {done1} rows",
+            "one_thread_rows_per_s": rows_s1}
+
+
+def read_traffic(name):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
+    path = os.path.join(ROOT, "profiles", f"pmc_sample_rows_{name}.txt")
+    if not os.path.exists(path):
+        return None
+    for line in open(path):
+        if line.startswith("traffic_bytes_per_launch:"):
+            try:
+                return float(line.split(":", 1)[1].strip())
+            except ValueError:
+                return None
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", default="qwen7b_batched_topk_topp", choices=sorted(WORKLOADS))
+    ap.add_argument("--sets", type=int, default=2, help="rotating input sets")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this benchmark runs on one GPU only: the sampler is measured "
+                          "on one MI355X; rows are independent, so a multi-GPU run would be "
+                          "batch-sharded with no exchange (see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    from lal_amd import abi
+    w = WORKLOADS[args.workload]
+    dev = abi.Device(0, max_batch=w["B"], max_vocab=w["V"])
+    sets = [Inputs(dev, w, 1000 + 17 * i) for i in range(max(1, args.sets))]
+    ios = [s.io(w) for s in sets]
+    params = params_for(w)
+
+    for i in range(args.warmup):
+        dev.sample(w["B"], w["V"], params, ios[i % len(ios)])
+    dev.sync()
+    abi.check(dev.lib.lal_gpu_device_sync(), "sync")
+    e0, e1 = dev.event(), dev.event()
+    t0 = time.perf_counter()
+    dev.record(e0)
+    for i in range(args.steps):
+        dev.sample(w["B"], w["V"], params, ios[i % len(ios)])
+    dev.record(e1)
+    dev.sync()
+    abi.check(dev.lib.lal_gpu_device_sync(), "sync")
+    wall = time.perf_counter() - t0
+    ms_total = dev.elapsed_ms(e0, e1)
+    ms_step = ms_total / args.steps
+    rows_per_s = w["B"] * args.steps / (ms_total / 1e3)
+
+    bytes_step = algorithmic_bytes_per_step(w)
+    achieved = bytes_step / (ms_step / 1e3) / 1e9
+    traffic = read_traffic(args.workload)
+    out = {
+        "metric": "sampled rows/sec + achieved HBM GB/s (% peak), vocab 152064, batch 1024, 1 GPU",
+        "value": rows_per_s,
+        "unit": "rows/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms_step,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic (GPU-generated, seeded)",
+        "config": {"workload": args.workload, "batch": w["B"], "vocab": w["V"],
+                   "logits": w["kind"], "temperature": w["T"], "top_k": w["k"],
+                   "top_p": w["top_p"], "rep_penalty": w["pen"], "history_ids": w["H"],
+                   "rotating_input_sets": len(sets),
+                   "live_input_bytes": len(sets) * 4 * w["B"] * w["V"],
+                   **({"allow_p": w["allow"], "bias_nnz": w["bias_nnz"],
+                       "mask_recent": w["mask_recent"]} if w.get("allow") else {})},
+        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
+                     "algorithmic_bytes_per_launch": bytes_step,
+                     "kernel": "sample_rows_kernel", "avg_launch_ms": ms_step},
+        "wall_s_timed_region": wall,
+    }
+    if not args.no_cpu_baseline:
+        out["cpu_baseline"] = cpu_baseline(w, dev, sets[0])
+    else:
+        out["cpu_baseline"] = None
+    print(json.dumps(out))
+    dev.close()
+
+
+if __name__ == "__main__":
+    main()

@@ -42,19 +42,23 @@ namespace {
 
 constexpr int WG = 256;             // threads per workgroup: 4 wave64
 constexpr int NWAVE = WG / 64;
-constexpr int U4 = 8;               // float4 loads per thread per tile
-constexpr int VPT = 4 * U4;         // values per thread per tile
-constexpr int TILE = WG * VPT;      // 8192 floats per tile
-constexpr int CAP = 2048;           // LDS candidate buffer entries
-constexpr int PER = CAP / WG;       // buffer entries per thread
+constexpr int U4 = 4;               // float4 loads per lane per wave-iteration
+constexpr int VPL = 4 * U4;         // values per lane per wave-iteration
+constexpr int WITER = 64 * U4;      // float4 per wave-iteration (1024 floats)
 constexpr int HBITS = 10;
-constexpr int HSLOTS = 1 << HBITS;  // LDS hash slots (>= 2 x distinct ids)
+constexpr int HSLOTS = 1 << HBITS;  // LDS hash slots
 constexpr int HCOUNT_MASK = 0xFFFF;
 constexpr int HF_MASKPRE = 1 << 16; // id is -inf before selection
 constexpr int HF_BAN = 1 << 17;     // id is dropped from the top-k pool
+constexpr int EP_ALL = HSLOTS + NWAVE * 256;  // epilogue scratch floats (hval + histograms)
+constexpr int RS_CHUNK = NWAVE * 256;         // rescan chunk (lives in the histogram area)
+// per-wave candidate buffer entries: 512 when k <= 128, 2048 up to LAL_GPU_MAX_K
+constexpr int CAPW_SMALL = 512;
+constexpr int CAPW_LARGE = 2048;
+constexpr int K_SMALL_MAX = 128;
 
 static_assert(2 * HSLOTS >= 3 * (LAL_GPU_MAX_HISTORY + LAL_GPU_MAX_BAN_IDS), "hash load <= 2/3");
-static_assert(CAP >= 2 * LAL_GPU_MAX_K, "buffer must hold twice the largest k");
+static_assert(CAPW_SMALL > K_SMALL_MAX && CAPW_LARGE > LAL_GPU_MAX_K, "buffer above k");
 
 // ---------------------------------------------------------------------------
 // expf as glibc computes it (the reference calls glibc's expf).  This is the
@@ -125,6 +129,15 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
 __device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
 
+// Orders this wave's LDS accesses before/after the point (lanes of one wave
+// exchange data through LDS without a workgroup barrier).
+__device__ __forceinline__ void wave_sync()
+{
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 __device__ __forceinline__ int wave_incl_scan(int v)
 {
     const int lane = lane_id();
@@ -157,21 +170,36 @@ __device__ __forceinline__ int wave_sum(int v)
     return v;
 }
 
+__device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
+__device__ __forceinline__ float readlane_f(float v, int l)
+{
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
+}
+
+template <int CAPW>
 struct Smem {
-    float cval[CAP];      // candidate values (exact processed logits)
-    int cidx[CAP];        // candidate token ids
-    float ep[CAP];        // epilogue scratch: probabilities, prefix sums
-    int hkey[HSLOTS];     // hash: token id or -1
-    int hinfo[HSLOTS];    // occurrence count | HF_* flags
-    float hval[HSLOTS];   // exact processed logit of the id
-    unsigned rhist[256];  // radix histogram
-    int wsum[2][NWAVE];   // block-scan wave totals (double-buffered)
+    float cval[NWAVE * CAPW];  // per-wave candidate buffers: exact processed logits
+    int cidx[NWAVE * CAPW];    // ... and their token ids
+    int hkey[HSLOTS];          // hash: token id or -1
+    int hinfo[HSLOTS];         // occurrence count | HF_* flags
+    union {
+        struct {
+            float hval[HSLOTS];            // exact processed logit of the id
+            unsigned whist[NWAVE][256];    // per-wave radix histograms
+        } h;
+        float ep[EP_ALL];                  // epilogue scratch (after streaming)
+    } u;
+    int wcnt[NWAVE];      // entries in each wave buffer (dead ones are nan)
+    int walive[NWAVE];    // live entries
+    unsigned tau_key;     // max over the waves' thresholds (order-preserving key)
+    float wtau[NWAVE];
+    int wstrict[NWAVE];
+    int wsum[2][NWAVE];
     float redf[NWAVE];
     int redi[NWAVE];
     int redi2[NWAVE];
     int sel_digit;
     int sel_rem;
-    int bcast;
 };
 
 struct KArgs {
@@ -207,8 +235,9 @@ struct KArgs {
     int any_bans;
 };
 
-// block reductions (one barrier each; callers keep control flow uniform)
-__device__ __forceinline__ float block_max(Smem &S, float v)
+// block reductions (barriers inside; callers keep control flow uniform)
+template <class SM>
+__device__ __forceinline__ float block_max(SM &S, float v)
 {
     v = wave_max(v);
     __syncthreads();
@@ -220,7 +249,8 @@ __device__ __forceinline__ float block_max(Smem &S, float v)
     return r;
 }
 
-__device__ __forceinline__ int block_min(Smem &S, int v)
+template <class SM>
+__device__ __forceinline__ int block_min(SM &S, int v)
 {
     v = wave_min(v);
     __syncthreads();
@@ -232,7 +262,8 @@ __device__ __forceinline__ int block_min(Smem &S, int v)
     return r;
 }
 
-__device__ __forceinline__ int block_sum(Smem &S, int v)
+template <class SM>
+__device__ __forceinline__ int block_sum(SM &S, int v)
 {
     v = wave_sum(v);
     __syncthreads();
@@ -269,25 +300,25 @@ __device__ __forceinline__ uint32_t hslot(int key)
     return ((uint32_t)key * 2654435761u) >> (32 - HBITS);
 }
 
-__device__ void hash_insert(Smem &S, int key, int add, int flags)
+__device__ __forceinline__ void hash_insert(int *hkey, int *hinfo, int key, int add, int flags)
 {
     uint32_t s = hslot(key);
     for (int probe = 0; probe < HSLOTS; ++probe) {
-        const int prev = atomicCAS(&S.hkey[s], -1, key);
+        const int prev = atomicCAS(&hkey[s], -1, key);
         if (prev == -1 || prev == key) {
-            if (add) atomicAdd(&S.hinfo[s], add);
-            if (flags) atomicOr(&S.hinfo[s], flags);
+            if (add) atomicAdd(&hinfo[s], add);
+            if (flags) atomicOr(&hinfo[s], flags);
             return;
         }
         s = (s + 1) & (HSLOTS - 1);
     }
 }
 
-__device__ __forceinline__ int hash_find(const Smem &S, int key)
+__device__ __forceinline__ int hash_find(const int *hkey, int key)
 {
     uint32_t s = hslot(key);
     for (int probe = 0; probe < HSLOTS; ++probe) {
-        const int k = S.hkey[s];
+        const int k = hkey[s];
         if (k == key) return (int)s;
         if (k == -1) return -1;
         s = (s + 1) & (HSLOTS - 1);
@@ -308,35 +339,324 @@ __device__ __forceinline__ float penalise(float x, int count, float pen)
     return x;
 }
 
-// ---------------------------------------------------------------------------
-// Block-wide radix select: k-th largest key over the LDS buffer [0, cnt) and
-// the register values v[i] whose bit is set in m.  Requires >= k inputs.
-// ---------------------------------------------------------------------------
-template <int NV>
-__device__ uint32_t block_kth_key(Smem &S, int cnt, const float (&v)[NV], uint64_t m, int k)
+__device__ __forceinline__ bool passes(float y, float tau, bool strict)
 {
+    return strict ? (y > tau) : (y >= tau);
+}
+
+// Sequential fp32 prefix sums over ep[0..n) in index order, done by wave 0
+// (lane l of a 64-chunk receives the running sum after element base+l).  The
+// additions happen in exactly the order of the reference's scalar loop.
+// Entries < 0 mark "not in the set" and are skipped.  Writes the inclusive
+// prefix back into ep and returns the total to every thread.
+template <class SM>
+__device__ __forceinline__ float block_seq_prefix(SM &S, float *ep, int n, float carry_in)
+{
+    __syncthreads();
+    if (wave_id() == 0) {
+        float acc = carry_in;
+        for (int base = 0; base < n; base += 64) {
+            const int i = base + lane_id();
+            const float e = (i < n) ? ep[i] : -1.0f;
+            const unsigned long long live = __ballot(!(e < 0.0f));
+            float pre = acc;
+            if (live) {
+                const int lim = min(64, n - base);
+                const int me = lane_id();
+                for (int l = 0; l < lim; ++l) {
+                    const float el = readlane_f(e, l);
+                    if (!(el < 0.0f)) acc = acc + el;
+                    if (me == l) pre = acc;
+                }
+            }
+            if (i < n) ep[i] = pre;
+        }
+        if (lane_id() == 0) S.redf[0] = acc;
+    }
+    __syncthreads();
+    const float tot = S.redf[0];
+    __syncthreads();
+    return tot;
+}
+
+// Inclusive sequential prefix over the lanes of one wave (lane order), values
+// < 0 skipped; returns this lane's running sum, *total the sum over all lanes.
+__device__ __forceinline__ float wave_seq_prefix(float e, int n, float *total)
+{
+    float acc = 0.0f, pre = 0.0f;
+    const int me = lane_id();
+    for (int l = 0; l < n; ++l) {
+        const float el = readlane_f(e, l);
+        if (!(el < 0.0f)) acc = acc + el;
+        if (me == l) pre = acc;
+    }
+    *total = acc;
+    return pre;
+}
+
+// ---------------------------------------------------------------------------
+// Element addressing for a row: [0, head) scalar head elements, then nb4
+// aligned float4 chunks, then a scalar tail of < 4 elements.
+// ---------------------------------------------------------------------------
+struct RowGeo {
+    int head, nb4, tail0, ntail;
+};
+
+__device__ __forceinline__ RowGeo row_geo(const float *row, int V)
+{
+    RowGeo g;
+    const int mis = (int)(((uintptr_t)row >> 2) & 3);
+    g.head = min((4 - mis) & 3, V);
+    g.nb4 = (V - g.head) >> 2;
+    g.tail0 = g.head + 4 * g.nb4;
+    g.ntail = V - g.tail0;
+    return g;
+}
+
+__device__ __forceinline__ int extra_elem(const RowGeo &g, int t)
+{
+    if (t < g.head) return t;
+    if (t < g.head + g.ntail) return g.tail0 + (t - g.head);
+    return -1;
+}
+
+// cheap upper bound of the processed logit: raw + bias, -inf if not allowed
+template <bool HAS_BIAS, bool HAS_ALLOW>
+__device__ __forceinline__ float upper_bound(const float *bias, const uint32_t *abits, int e, float x)
+{
+    float y = x;
+    if (HAS_BIAS) y = y + bias[e];
+    if (HAS_ALLOW) {
+        if (!allow_bit(abits, e)) y = -INFINITY;
+    }
+    return y;
+}
+
+// exact processed value for a value that passed the upper-bound filter
+__device__ __forceinline__ float exact_value(const int *hkey, const float *hval, bool use_hash, int e,
+                                             float yhat)
+{
+    if (use_hash) {
+        const int s = hash_find(hkey, e);
+        if (s >= 0) return hval[s];
+    }
+    return yhat;
+}
+
+// ---------------------------------------------------------------------------
+// Per-wave state and candidate buffer
+// ---------------------------------------------------------------------------
+struct WState {
+    float tau;   // running lower bound of the row's k-th largest processed logit
+    int strict;  // 1: buffer holds values > tau (more than CAPW tie at tau)
+    int cnt;     // entries in the wave's buffer
+};
+
+// Wave radix select: k-th largest key over bv[0..cnt) and the lanes' values
+// y[i] with bit i of m set.  Requires >= k inputs.  Wave-synchronous.
+template <int NV>
+__device__ __forceinline__ uint32_t wave_kth_key(unsigned *hist, const float *bv, int cnt,
+                                                 const float (&y)[NV], uint32_t m, int k)
+{
+    uint32_t prefix = 0, pmask = 0;
+    int rem = k;
+    const int lane = lane_id();
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        hist[4 * lane + 0] = 0;
+        hist[4 * lane + 1] = 0;
+        hist[4 * lane + 2] = 0;
+        hist[4 * lane + 3] = 0;
+        wave_sync();
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if ((m >> i) & 1u) {
+                const uint32_t key = fkey(y[i]);
+                if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+            }
+        }
+        for (int j = lane; j < cnt; j += 64) {
+            const float v = bv[j];
+            if (v != v) continue;
+            const uint32_t key = fkey(v);
+            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+        }
+        wave_sync();
+        const int b0 = 255 - 4 * lane;
+        const int h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
+        const int lsum = h0 + h1 + h2 + h3;
+        const int incl = wave_incl_scan(lsum);
+        const int excl = incl - lsum;
+        const bool hit = (excl < rem && rem <= incl);
+        int r = rem - excl, d = b0;
+        if (r <= h0) d = b0;
+        else if ((r -= h0) <= h1) d = b0 - 1;
+        else if ((r -= h1) <= h2) d = b0 - 2;
+        else { r -= h2; d = b0 - 3; }
+        const unsigned long long hm = __ballot(hit);
+        const int src = hm ? (int)__builtin_ctzll(hm) : 0;
+        d = readlane_i(d, src);
+        r = readlane_i(r, src);
+        prefix |= (uint32_t)d << shift;
+        pmask |= 0xFFu << shift;
+        rem = r;
+        wave_sync();
+    }
+    return prefix;
+}
+
+// Buffer entries whose id carries UNREFINED hold the cheap upper bound (raw
+// logit + bias, allow mask applied); their exact value (penalty, pre-selection
+// bans) is looked up only when the wave must select or at the end.  A refined
+// entry that fails the current threshold becomes dead (value nan).
+constexpr int UNREFINED = (int)0x80000000;
+
+__device__ __forceinline__ void wave_refine(float *bv, int *bi, int cnt, const int *hkey,
+                                            const float *hval, float tau, bool strict)
+{
+    for (int j = lane_id(); j < cnt; j += 64) {
+        const int id = bi[j];
+        if (!(id & UNREFINED)) continue;
+        const int e = id & ~UNREFINED;
+        const float y = exact_value(hkey, hval, true, e, bv[j]);
+        bv[j] = passes(y, tau, strict) ? y : NAN;
+        bi[j] = e;
+    }
+    wave_sync();
+}
+
+// Offer this wave's values to its buffer.  x[i] are upper bounds whose pass
+// bit is set in m.  On overflow the wave refines its buffer and the offered
+// values, raises tau to the k-th largest of them and compacts.
+// Wave-synchronous, no workgroup barrier.
+template <int NQ, int CAPW>
+__device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, const int *hkey,
+                                           const float *hval, bool use_hash, const float (&x)[4 * NQ],
+                                           const int (&eb)[NQ], uint32_t m, WState &st, int k,
+                                           unsigned *tau_key_shared)
+{
+    constexpr int NV = 4 * NQ;
+    const int tag = use_hash ? UNREFINED : 0;
+    int c = __popc(m);
+    int incl = wave_incl_scan(c);
+    int total = readlane_i(incl, 63);
+    if (total == 0) return;
+    if (st.cnt + total <= CAPW) {
+        int pos = st.cnt + incl - c;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if ((m >> i) & 1u) {
+                bv[pos] = x[i];
+                bi[pos] = (eb[i >> 2] + (i & 3)) | tag;
+                pos++;
+            }
+        }
+        st.cnt += total;
+        wave_sync();
+        return;
+    }
+    // overflow: exact values first
+    float y[NV];
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        y[i] = x[i];
+        if ((m >> i) & 1u) {
+            const int e = eb[i >> 2] + (i & 3);
+            y[i] = exact_value(hkey, hval, use_hash, e, x[i]);
+            if (!passes(y[i], st.tau, st.strict)) m &= ~(1u << i);
+        }
+    }
+    wave_sync();
+    if (use_hash) wave_refine(bv, bi, st.cnt, hkey, hval, st.tau, st.strict);
+    int alive = 0;
+    for (int j = lane_id(); j < st.cnt; j += 64) alive += (bv[j] == bv[j]);
+    alive = wave_sum(alive);
+    c = __popc(m);
+    total = wave_sum(c);
+    constexpr int R = CAPW / 64;
+    float rb[R];
+    int ri[R];
+    const int lane = lane_id();
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        const int j = lane + 64 * r;
+        rb[r] = (j < st.cnt) ? bv[j] : NAN;
+        ri[r] = (j < st.cnt) ? bi[j] : -1;
+    }
+    float tk = st.tau;
+    bool strict = st.strict;
+    if (alive + total > CAPW) {
+        tk = keyf(wave_kth_key<NV>(hist, bv, st.cnt, y, m, k));
+        int nge = 0;
+#pragma unroll
+        for (int r = 0; r < R; ++r) nge += (rb[r] >= tk);
+#pragma unroll
+        for (int i = 0; i < NV; ++i)
+            if ((m >> i) & 1u) nge += (y[i] >= tk);
+        strict = wave_sum(nge) > CAPW;
+    }
+    // keep buffer entries and offered values that pass (tk, strict)
+    int mine = 0;
+#pragma unroll
+    for (int r = 0; r < R; ++r) mine += passes(rb[r], tk, strict);
+#pragma unroll
+    for (int i = 0; i < NV; ++i)
+        if ((m >> i) & 1u) mine += passes(y[i], tk, strict);
+    const int incl2 = wave_incl_scan(mine);
+    const int tot2 = readlane_i(incl2, 63);
+    int pos = incl2 - mine;
+    wave_sync();  // every lane holds its buffer entries in registers
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+        if (passes(rb[r], tk, strict)) {
+            bv[pos] = rb[r];
+            bi[pos] = ri[r];
+            pos++;
+        }
+    }
+#pragma unroll
+    for (int i = 0; i < NV; ++i) {
+        if (((m >> i) & 1u) && passes(y[i], tk, strict)) {
+            bv[pos] = y[i];
+            bi[pos] = eb[i >> 2] + (i & 3);
+            pos++;
+        }
+    }
+    wave_sync();
+    st.cnt = tot2;
+    if (tk != st.tau || strict != (bool)st.strict) {
+        st.tau = tk;
+        st.strict = strict ? 1 : 0;
+        if (lane == 0) atomicMax(tau_key_shared, fkey(tk));
+    }
+}
+
+// Block radix select over the union of the wave buffers (each thread reads
+// its own wave's entries).  Requires >= k entries in total.
+template <int CAPW, class SM>
+__device__ __forceinline__ uint32_t block_kth_union(SM &S, int k)
+{
+    unsigned *hist = S.u.h.whist[0];
+    const int w = wave_id(), lane = lane_id();
+    const int cnt = S.wcnt[w];
+    const float *bv = S.cval + w * CAPW;
     uint32_t prefix = 0, pmask = 0;
     int rem = k;
     for (int pass = 0; pass < 4; ++pass) {
         const int shift = 24 - 8 * pass;
-        S.rhist[threadIdx.x] = 0;
         __syncthreads();
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            if ((m >> i) & 1ull) {
-                const uint32_t key = fkey(v[i]);
-                if ((key & pmask) == prefix) atomicAdd(&S.rhist[(key >> shift) & 255u], 1u);
-            }
-        }
-        for (int j = threadIdx.x; j < cnt; j += WG) {
-            const uint32_t key = fkey(S.cval[j]);
-            if ((key & pmask) == prefix) atomicAdd(&S.rhist[(key >> shift) & 255u], 1u);
+        hist[threadIdx.x] = 0;
+        __syncthreads();
+        for (int j = lane; j < cnt; j += 64) {
+            const float v = bv[j];
+            if (v != v) continue;
+            const uint32_t key = fkey(v);
+            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
         }
         __syncthreads();
-        if (threadIdx.x < 64) {
-            const int b0 = 255 - 4 * lane_id();
-            const int h0 = S.rhist[b0], h1 = S.rhist[b0 - 1], h2 = S.rhist[b0 - 2],
-                      h3 = S.rhist[b0 - 3];
+        if (w == 0) {
+            const int b0 = 255 - 4 * lane;
+            const int h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
             const int lsum = h0 + h1 + h2 + h3;
             const int incl = wave_incl_scan(lsum);
             const int excl = incl - lsum;
@@ -355,169 +675,27 @@ __device__ uint32_t block_kth_key(Smem &S, int cnt, const float (&v)[NV], uint64
         pmask |= 0xFFu << shift;
         rem = S.sel_rem;
     }
+    __syncthreads();
     return prefix;
-}
-
-// Sequential fp32 prefix sums over S.ep[0..n) in index order, done by wave 0
-// (lane l of a 64-chunk receives the running sum after element base+l).  The
-// additions happen in exactly the order of the reference's scalar loop.
-// Entries < 0 are "not in the set" markers and are skipped.  Writes the
-// inclusive prefix back into S.ep and returns the total to every thread.
-__device__ float block_seq_prefix(Smem &S, int n, float carry_in)
-{
-    __syncthreads();
-    if (wave_id() == 0) {
-        float acc = carry_in;
-        for (int base = 0; base < n; base += 64) {
-            const int i = base + lane_id();
-            const float e = (i < n) ? S.ep[i] : -1.0f;
-            const unsigned long long live = __ballot(!(e < 0.0f));
-            float pre = acc;
-            if (live) {
-                const int ebits = __float_as_int(e);
-                const int lim = min(64, n - base);
-                const int me = lane_id();
-                for (int l = 0; l < lim; ++l) {
-                    const float el = __int_as_float(__builtin_amdgcn_readlane(ebits, l));
-                    if (!(el < 0.0f)) acc = acc + el;
-                    if (me == l) pre = acc;
-                }
-            }
-            if (i < n) S.ep[i] = pre;
-        }
-        if (lane_id() == 0) S.redf[0] = acc;
-    }
-    __syncthreads();
-    const float tot = S.redf[0];
-    __syncthreads();
-    return tot;
-}
-
-// ---------------------------------------------------------------------------
-// Element addressing for a row: [0, head) scalar head elements, then nb4
-// aligned float4 chunks, then a scalar tail of < 4 elements.  Head and tail
-// ("extra") elements ride along as one more value slot of tile 0.
-// ---------------------------------------------------------------------------
-struct RowGeo {
-    int head, nb4, tail0, ntail, ntiles;
-};
-
-__device__ __forceinline__ RowGeo row_geo(const float *row, int V)
-{
-    RowGeo g;
-    const int mis = (int)(((uintptr_t)row >> 2) & 3);
-    g.head = min((4 - mis) & 3, V);
-    g.nb4 = (V - g.head) >> 2;
-    g.tail0 = g.head + 4 * g.nb4;
-    g.ntail = V - g.tail0;
-    g.ntiles = max(1, (g.nb4 + TILE / 4 - 1) / (TILE / 4));
-    return g;
-}
-
-__device__ __forceinline__ int extra_elem(const RowGeo &g, int t)
-{
-    if (t < g.head) return t;
-    if (t < g.head + g.ntail) return g.tail0 + (t - g.head);
-    return -1;
-}
-
-template <bool HAS_BIAS, bool HAS_ALLOW>
-__device__ __forceinline__ float upper_bound(const KArgs &A, const uint32_t *abits, int e, float x)
-{
-    float y = x;
-    if (HAS_BIAS) y = y + A.bias[e];
-    if (HAS_ALLOW) {
-        if (!allow_bit(abits, e)) y = -INFINITY;
-    }
-    return y;
-}
-
-// exact processed value for a value that passed the upper-bound filter
-__device__ __forceinline__ float exact_value(const Smem &S, bool use_hash, int e, float yhat)
-{
-    if (use_hash) {
-        const int s = hash_find(S, e);
-        if (s >= 0) return S.hval[s];
-    }
-    return yhat;
-}
-
-__device__ __forceinline__ bool passes(float y, float tau, bool strict)
-{
-    return strict ? (y > tau) : (y >= tau);
-}
-
-// Load tile `t` of the row into y[0..VPT) (+ y[VPT] for the extra slot),
-// replacing each value by its exact processed value when it passes (tau,
-// strict), and NaN when it is out of range or fails.  Returns the pass mask.
-template <bool HAS_BIAS, bool HAS_ALLOW>
-__device__ __forceinline__ uint64_t load_tile(const KArgs &A, const Smem &S, const float *row,
-                                              const uint32_t *abits, const RowGeo &g, int t,
-                                              float tau, bool strict, bool use_hash,
-                                              float (&y)[VPT + 1])
-{
-    const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
-    f32x4 xv[U4];
-#pragma unroll
-    for (int u = 0; u < U4; ++u) {
-        const int q = t * (TILE / 4) + u * WG + (int)threadIdx.x;
-        if (q < g.nb4) xv[u] = __builtin_nontemporal_load(row4 + q);
-        else xv[u] = f32x4{NAN, NAN, NAN, NAN};
-    }
-    uint64_t m = 0;
-#pragma unroll
-    for (int u = 0; u < U4; ++u) {
-        const int q = t * (TILE / 4) + u * WG + (int)threadIdx.x;
-        const int e0 = g.head + 4 * q;
-        const float xs[4] = {xv[u].x, xv[u].y, xv[u].z, xv[u].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            const int i = 4 * u + c;
-            float yy = xs[c];
-            if (q < g.nb4) {
-                yy = upper_bound<HAS_BIAS, HAS_ALLOW>(A, abits, e0 + c, yy);
-                if (passes(yy, tau, strict)) {
-                    yy = exact_value(S, use_hash, e0 + c, yy);
-                    if (passes(yy, tau, strict)) m |= 1ull << i;
-                }
-            }
-            y[i] = yy;
-        }
-    }
-    // extra slot (head / tail elements) in tile 0
-    y[VPT] = NAN;
-    if (t == 0) {
-        const int e = extra_elem(g, threadIdx.x);
-        if (e >= 0) {
-            float yy = upper_bound<HAS_BIAS, HAS_ALLOW>(A, abits, e, row[e]);
-            if (passes(yy, tau, strict)) {
-                yy = exact_value(S, use_hash, e, yy);
-                if (passes(yy, tau, strict)) m |= 1ull << VPT;
-            }
-            y[VPT] = yy;
-        }
-    }
-    return m;
-}
-
-__device__ __forceinline__ int tile_elem(const RowGeo &g, int t, int i)
-{
-    if (i == VPT) return extra_elem(g, threadIdx.x);
-    const int u = i >> 2, c = i & 3;
-    const int q = t * (TILE / 4) + u * WG + (int)threadIdx.x;
-    return g.head + 4 * q + c;
 }
 
 // ---------------------------------------------------------------------------
 // Rescan path: finish the row by re-reading it in id order (used when more
-// than CAP logits tie at the threshold, so the pool is not in LDS).
+// tokens tie at the threshold than the buffers hold).
 // ---------------------------------------------------------------------------
-template <bool HAS_BIAS, bool HAS_ALLOW>
-__device__ float rescan_value(const KArgs &A, const Smem &S, const float *row, const uint32_t *abits,
-                              bool use_hash, int e, float x)
+template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
+__device__ __forceinline__ float rescan_value(const KArgs &A, const SM &S, const float *row,
+                                              const uint32_t *abits, bool use_hash, int e)
 {
-    const float yh = upper_bound<HAS_BIAS, HAS_ALLOW>(A, abits, e, x);
-    return exact_value(S, use_hash, e, yh);
+    const float yh = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
+    return exact_value(S.hkey, S.u.h.hval, use_hash, e, yh);
+}
+
+template <class SM>
+__device__ __forceinline__ bool is_banned(const SM &S, int e)
+{
+    const int s = hash_find(S.hkey, e);
+    return s >= 0 && (S.hinfo[s] & HF_BAN);
 }
 
 struct RescanStats {
@@ -527,21 +705,18 @@ struct RescanStats {
     int first_max_kept; // smallest id attaining max_kept
 };
 
-template <bool HAS_BIAS, bool HAS_ALLOW>
-__device__ RescanStats rescan_stats(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
-                                    const RowGeo &g, bool use_hash, float T, bool use_ban)
+template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
+__device__ __forceinline__ RescanStats rescan_stats(const KArgs &A, SM &S, const float *row,
+                                                    const uint32_t *abits, bool use_hash, float T,
+                                                    bool use_ban)
 {
     int nc = 0, nk = 0, first = INT_MAX;
     float mk = -INFINITY;
-    // pass 1: counts, max and first id
     for (int e = threadIdx.x; e < A.V; e += WG) {
-        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
+        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
         if (!(yv >= T)) continue;
         nc++;
-        if (use_ban) {
-            const int s = hash_find(S, e);
-            if (s >= 0 && (S.hinfo[s] & HF_BAN)) continue;
-        }
+        if (use_ban && is_banned(S, e)) continue;
         nk++;
         mk = fmaxf(mk, yv);
         first = min(first, e);
@@ -553,12 +728,9 @@ __device__ RescanStats rescan_stats(const KArgs &A, Smem &S, const float *row, c
     st.first_kept = block_min(S, first);
     int fm = INT_MAX;
     for (int e = threadIdx.x; e < A.V; e += WG) {
-        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
+        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
         if (!(yv >= T) || !(yv == st.max_kept)) continue;
-        if (use_ban) {
-            const int s = hash_find(S, e);
-            if (s >= 0 && (S.hinfo[s] & HF_BAN)) continue;
-        }
+        if (use_ban && is_banned(S, e)) continue;
         fm = min(fm, e);
     }
     st.first_max_kept = block_min(S, fm);
@@ -566,16 +738,15 @@ __device__ RescanStats rescan_stats(const KArgs &A, Smem &S, const float *row, c
 }
 
 // Sequential sum (draw == false) or draw (draw == true) over the row in id
-// order, 1024 ids at a time.  Returns the sum; with draw, *token receives the
-// first kept id whose running sum reaches r (-1 when none does).
-constexpr int RS_CHUNK = 1024;
-static_assert(RS_CHUNK <= CAP, "rescan chunk lives in S.ep");
-
-template <bool HAS_BIAS, bool HAS_ALLOW>
-__device__ float rescan_sequential(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
-                                   bool use_hash, float T, bool use_ban, float mx, bool draw,
-                                   float r, int *token)
+// order, RS_CHUNK ids at a time.  Returns the sum; with draw, *token receives
+// the first kept id whose running sum reaches r (-1 when none does).
+template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
+__device__ __forceinline__ float rescan_sequential(const KArgs &A, SM &S, const float *row,
+                                                   const uint32_t *abits, bool use_hash, float T,
+                                                   bool use_ban, float mx, bool draw, float r,
+                                                   int *token)
 {
+    float *ep = S.u.ep + HSLOTS;  // histogram area; hval stays intact
     float acc = 0.0f;
     int found = -1;
     for (int c0 = 0; c0 < A.V; c0 += RS_CHUNK) {
@@ -588,22 +759,18 @@ __device__ float rescan_sequential(const KArgs &A, Smem &S, const float *row, co
             kept[q] = false;
             if (i < n) {
                 const int e = c0 + i;
-                const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
-                kept[q] = (yv >= T);
-                if (kept[q] && use_ban) {
-                    const int s = hash_find(S, e);
-                    if (s >= 0 && (S.hinfo[s] & HF_BAN)) kept[q] = false;
-                }
-                S.ep[i] = kept[q] ? glibc_expf((yv - mx) / A.T) : -1.0f;
+                const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
+                kept[q] = (yv >= T) && !(use_ban && is_banned(S, e));
+                ep[i] = kept[q] ? glibc_expf((yv - mx) / A.T) : -1.0f;
             }
         }
-        acc = block_seq_prefix(S, n, acc);
+        acc = block_seq_prefix(S, ep, n, acc);
         if (draw) {
             int first = INT_MAX;
 #pragma unroll
             for (int q = 0; q < RS_CHUNK / WG; ++q) {
                 const int i = (int)threadIdx.x + q * WG;
-                if (i < n && kept[q] && r <= S.ep[i]) first = min(first, i);
+                if (i < n && kept[q] && r <= ep[i]) first = min(first, i);
             }
             first = block_min(S, first);
             if (first != INT_MAX) {
@@ -618,24 +785,27 @@ __device__ float rescan_sequential(const KArgs &A, Smem &S, const float *row, co
 
 // Candidate outputs for a rescanned row: the first cand_ld pool ids in id
 // order with their kept flag and probability e/sum.
-template <bool HAS_BIAS, bool HAS_ALLOW>
-__device__ void rescan_write_cands(const KArgs &A, Smem &S, const float *row, const uint32_t *abits,
-                                   bool use_hash, float T, bool use_ban, float mx, float sum,
-                                   bool greedy, int greedy_token, int b)
+template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
+__device__ __forceinline__ void rescan_write_cands(const KArgs &A, SM &S, const float *row,
+                                                   const uint32_t *abits, bool use_hash, float T,
+                                                   bool use_ban, float mx, float sum, bool greedy,
+                                                   int greedy_token, int b)
 {
+    constexpr int PT = RS_CHUNK / WG;
     int written = 0;
     for (int c0 = 0; c0 < A.V && written < A.cand_ld; c0 += RS_CHUNK) {
         const int n = min(RS_CHUNK, A.V - c0);
-        int e_of[RS_CHUNK / WG];
-        float y_of[RS_CHUNK / WG];
+        int e_of[PT];
+        float y_of[PT];
         int mine = 0;
 #pragma unroll
-        for (int q = 0; q < RS_CHUNK / WG; ++q) {
-            const int i = (int)threadIdx.x * (RS_CHUNK / WG) + q;  // contiguous ids per thread
+        for (int q = 0; q < PT; ++q) {
+            const int i = (int)threadIdx.x * PT + q;  // contiguous ids per thread
             e_of[q] = -1;
+            y_of[q] = 0.0f;
             if (i < n) {
                 const int e = c0 + i;
-                y_of[q] = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e, row[e]);
+                y_of[q] = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
                 if (y_of[q] >= T) {
                     e_of[q] = e;
                     mine++;
@@ -645,20 +815,11 @@ __device__ void rescan_write_cands(const KArgs &A, Smem &S, const float *row, co
         int tot;
         int pos = written + block_excl_scan(mine, tot, S.wsum[(c0 / RS_CHUNK) & 1]);
 #pragma unroll
-        for (int q = 0; q < RS_CHUNK / WG; ++q) {
+        for (int q = 0; q < PT; ++q) {
             if (e_of[q] < 0) continue;
             if (pos < A.cand_ld) {
                 const int e = e_of[q];
-                bool kept;
-                if (greedy) {
-                    kept = (e == greedy_token);
-                } else {
-                    kept = true;
-                    if (use_ban) {
-                        const int s = hash_find(S, e);
-                        if (s >= 0 && (S.hinfo[s] & HF_BAN)) kept = false;
-                    }
-                }
+                const bool kept = greedy ? (e == greedy_token) : !(use_ban && is_banned(S, e));
                 const size_t o = (size_t)b * A.cand_ld + pos;
                 if (A.cand_ids) A.cand_ids[o] = e;
                 if (A.cand_kept) A.cand_kept[o] = kept ? 1 : 0;
@@ -674,14 +835,223 @@ __device__ void rescan_write_cands(const KArgs &A, Smem &S, const float *row, co
 }
 
 // ---------------------------------------------------------------------------
-// The sampler kernel: one workgroup per row.
+// Epilogue over the pool (ids ascending in S.cidx[0..nc), values in S.cval)
+// when it fits one wave: one candidate per lane of wave 0, no barriers.
 // ---------------------------------------------------------------------------
-template <bool HAS_BIAS, bool HAS_ALLOW>
-__global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
+struct RowResult {
+    int token, n_kept;
+    float sum;
+};
+
+template <class SM>
+__device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc, float u, int b)
 {
-    __shared__ Smem S;
+    const int lane = lane_id();
+    const bool valid = lane < nc;
+    const float y = valid ? S.cval[lane] : -INFINITY;
+    const int id = valid ? S.cidx[lane] : -1;
+    const bool ban = valid && A.any_bans && is_banned(S, id);
+    bool nuc = valid;
+    if (A.top_p > 0.0f && A.top_p < 1.0f) {
+        // gpt2_server.c:2908-2955: probabilities over the pool, stable sort
+        // by descending probability, inclusive cumulative cutoff
+        float amax = wave_max(valid ? y : -INFINITY);
+        if (!(amax > -1e30f)) amax = -1e30f;
+        const float e1 = valid ? glibc_expf((y - amax) / A.T) : -1.0f;
+        float se;
+        (void)wave_seq_prefix(e1, nc, &se);
+        const float inv = 1.0f / (se + 1e-12f);
+        const float p = valid ? e1 * inv : 0.0f;
+        int rank = 0;
+        for (int j = 0; j < nc; ++j) {
+            const float pj = readlane_f(p, j);
+            rank += (pj > p) || (pj == p && j < lane);
+        }
+        float *ep = S.u.ep;
+        if (valid) ep[rank] = p;
+        wave_sync();
+        const float ps = valid ? ep[lane] : -1.0f;
+        float tot;
+        const float cum = wave_seq_prefix(ps, nc, &tot);
+        const unsigned long long reach = __ballot(valid && cum >= A.top_p);
+        const int cut = reach ? (int)__builtin_ctzll(reach) : nc - 1;
+        nuc = valid && rank <= cut;
+        wave_sync();
+    }
+    bool kept = nuc && !ban;
+    if (__ballot(kept) == 0ull) kept = valid;  // restore the top-k pool
+    const int n_kept = __popcll(__ballot(kept));
+    const float kmax = wave_max(kept ? y : -INFINITY);
+    const float mx = (kmax > -1e30f) ? kmax : -1e30f;
+    const float e2 = kept ? glibc_expf((y - mx) / A.T) : -1.0f;
+    float sum;
+    const float pre = wave_seq_prefix(e2, nc, &sum);
+    RowResult res;
+    res.n_kept = n_kept;
+    res.sum = sum;
+    if (A.variant == LAL_GPU_VARIANT_FILTERED && sum <= 0.0f) {
+        const unsigned long long hm = __ballot(kept && y == kmax && kmax > -1e30f);
+        res.token = hm ? readlane_i(id, (int)__builtin_ctzll(hm)) : 0;
+    } else {
+        const float r = u * sum;
+        if ((A.flags & LAL_GPU_F_DRAW_GPT2) && r == 0.0f) {
+            res.token = 0;
+        } else {
+            const unsigned long long hm = __ballot(kept && r <= pre);
+            res.token = hm ? readlane_i(id, (int)__builtin_ctzll(hm)) : A.V - 1;
+        }
+    }
+    if (valid && lane < A.cand_ld) {
+        const size_t o = (size_t)b * A.cand_ld + lane;
+        if (A.cand_ids) A.cand_ids[o] = id;
+        if (A.cand_kept) A.cand_kept[o] = kept ? 1 : 0;
+        if (A.cand_probs) A.cand_probs[o] = kept ? e2 / sum : 0.0f;
+    }
+    return res;
+}
+
+// General epilogue (pool above one wave): block-wide, PER entries per thread.
+template <int PER, class SM>
+__device__ __forceinline__ RowResult block_epilogue(const KArgs &A, SM &S, int nc, float u, int b)
+{
+    const int tid = threadIdx.x;
+    float *ep = S.u.ep;
+    float yv[PER];
+    bool nuc[PER], ban[PER], kept[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        const int j = tid + r * WG;
+        yv[r] = (j < nc) ? S.cval[j] : NAN;
+        nuc[r] = (j < nc);
+        ban[r] = (j < nc) && A.any_bans && is_banned(S, S.cidx[j]);
+    }
+    if (A.top_p > 0.0f && A.top_p < 1.0f) {
+        float lm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < PER; ++r)
+            if (tid + r * WG < nc) lm = fmaxf(lm, yv[r]);
+        float amax = block_max(S, lm);
+        if (!(amax > -1e30f)) amax = -1e30f;
+        float e1[PER];
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int j = tid + r * WG;
+            e1[r] = (j < nc) ? glibc_expf((yv[r] - amax) / A.T) : 0.0f;
+            if (j < nc) ep[j] = e1[r];
+        }
+        const float se = block_seq_prefix(S, ep, nc, 0.0f);
+        const float inv = 1.0f / (se + 1e-12f);
+        float pr[PER];
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int j = tid + r * WG;
+            pr[r] = e1[r] * inv;
+            if (j < nc) ep[j] = pr[r];
+        }
+        __syncthreads();
+        int prk[PER];
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int j = tid + r * WG;
+            prk[r] = -1;
+            if (j < nc) {
+                int rank = 0;
+                for (int q = 0; q < nc; ++q) {
+                    const float pq = ep[q];
+                    rank += (pq > pr[r]) || (pq == pr[r] && q < j);
+                }
+                prk[r] = rank;
+            }
+        }
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < PER; ++r)
+            if (prk[r] >= 0) ep[prk[r]] = pr[r];
+        block_seq_prefix(S, ep, nc, 0.0f);
+        int fc = INT_MAX;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int j = tid + r * WG;
+            if (j < nc && ep[j] >= A.top_p) fc = min(fc, j);
+        }
+        fc = block_min(S, fc);
+        const int cut = (fc == INT_MAX) ? nc - 1 : fc;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) nuc[r] = (prk[r] >= 0) && (prk[r] <= cut);
+    }
+    int lk = 0;
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        kept[r] = nuc[r] && !ban[r];
+        lk += kept[r];
+    }
+    RowResult res;
+    res.n_kept = block_sum(S, lk);
+    if (res.n_kept == 0) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) kept[r] = (tid + r * WG < nc);
+        res.n_kept = nc;
+    }
+    float lm = -INFINITY;
+#pragma unroll
+    for (int r = 0; r < PER; ++r)
+        if (kept[r]) lm = fmaxf(lm, yv[r]);
+    const float kmax = block_max(S, lm);
+    const float mx = (kmax > -1e30f) ? kmax : -1e30f;
+    float e2[PER];
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+        const int j = tid + r * WG;
+        e2[r] = kept[r] ? glibc_expf((yv[r] - mx) / A.T) : 0.0f;
+        if (j < nc) ep[j] = kept[r] ? e2[r] : -1.0f;
+    }
+    res.sum = block_seq_prefix(S, ep, nc, 0.0f);
+    if (A.variant == LAL_GPU_VARIANT_FILTERED && res.sum <= 0.0f) {
+        int cand = INT_MAX;
+#pragma unroll
+        for (int r = 0; r < PER; ++r)
+            if (kept[r] && yv[r] == kmax && kmax > -1e30f) cand = min(cand, tid + r * WG);
+        const int j = block_min(S, cand);
+        res.token = (j == INT_MAX) ? 0 : S.cidx[j];
+    } else {
+        const float rr = u * res.sum;
+        if ((A.flags & LAL_GPU_F_DRAW_GPT2) && rr == 0.0f) {
+            res.token = 0;
+        } else {
+            int cand = INT_MAX;
+#pragma unroll
+            for (int r = 0; r < PER; ++r)
+                if (kept[r] && rr <= ep[tid + r * WG]) cand = min(cand, tid + r * WG);
+            const int j = block_min(S, cand);
+            res.token = (j == INT_MAX) ? A.V - 1 : S.cidx[j];
+        }
+    }
+    if (A.cand_ld > 0) {
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int j = tid + r * WG;
+            if (j < nc && j < A.cand_ld) {
+                const size_t o = (size_t)b * A.cand_ld + j;
+                if (A.cand_ids) A.cand_ids[o] = S.cidx[j];
+                if (A.cand_kept) A.cand_kept[o] = kept[r] ? 1 : 0;
+                if (A.cand_probs) A.cand_probs[o] = kept[r] ? e2[r] / res.sum : 0.0f;
+            }
+        }
+    }
+    return res;
+}
+
+// ---------------------------------------------------------------------------
+// The sampler kernel: one workgroup (four wave64) per row.
+// ---------------------------------------------------------------------------
+template <bool HAS_BIAS, bool HAS_ALLOW, int CAPW>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_rows_kernel(KArgs A)
+{
+    __shared__ Smem<CAPW> S;
+    constexpr int PER = NWAVE * CAPW / WG;  // union entries per thread
     const int b = blockIdx.x;
     const int tid = threadIdx.x;
+    const int w = wave_id(), lane = lane_id();
     const int V = A.V;
     const float *row = A.logits + (size_t)b * A.ld;
     const uint32_t *abits = HAS_ALLOW ? A.allow + (size_t)b * A.allow_ld : nullptr;
@@ -691,12 +1061,28 @@ __global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
         nh = A.hist_len ? A.hist_len[b] : A.hist_ld;
         nh = max(0, min(nh, A.hist_ld));
     }
+    const RowGeo g = row_geo(row, V);
+    const int k = A.greedy ? 1 : min(max(A.k, 1), V);
+
+    // this wave's contiguous share of the aligned body
+    const int qb = (int)(((long long)g.nb4 * w) / NWAVE);
+    const int qe = (int)(((long long)g.nb4 * (w + 1)) / NWAVE);
+    const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
+
+    // first iteration's loads go out before the hash setup
+    f32x4 cur[U4];
+#pragma unroll
+    for (int u = 0; u < U4; ++u) {
+        const int q = qb + u * 64 + lane;
+        cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+    }
 
     // ---- setup: hash of history / ban ids -------------------------------
     for (int s = tid; s < HSLOTS; s += WG) {
         S.hkey[s] = -1;
         S.hinfo[s] = 0;
     }
+    if (tid == 0) S.tau_key = 0u;  // below every real key
     __syncthreads();
     for (int i = tid; i < nh; i += WG) {
         const int t = hrow[i];
@@ -705,11 +1091,11 @@ __global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
         if (A.mask_recent > 0 && i >= nh - A.mask_recent) flags |= HF_MASKPRE;
         if (A.ban_last && i == nh - 1) flags |= HF_BAN;
         if (A.ban_repeat > 0 && i >= nh - A.ban_repeat) flags |= HF_BAN;
-        hash_insert(S, t, A.apply_pen ? 1 : 0, flags);
+        hash_insert(S.hkey, S.hinfo, t, A.apply_pen ? 1 : 0, flags);
     }
     for (int i = tid; i < A.n_ban; i += WG) {
         const int t = A.ban_ids[i];
-        if (t >= 0 && t < V) hash_insert(S, t, 0, HF_BAN);
+        if (t >= 0 && t < V) hash_insert(S.hkey, S.hinfo, t, 0, HF_BAN);
     }
     __syncthreads();
     int nocc = 0;
@@ -722,153 +1108,163 @@ __global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
         if (HAS_BIAS) yv = yv + A.bias[key];
         if (HAS_ALLOW && !allow_bit(abits, key)) yv = -INFINITY;
         if (info & HF_MASKPRE) yv = -INFINITY;
-        S.hval[s] = yv;
+        S.u.h.hval[s] = yv;
     }
     const bool use_hash = block_sum(S, nocc) > 0;
 
-    // ---- stream the row -----------------------------------------------------
-    const RowGeo g = row_geo(row, V);
-    const int k = A.greedy ? 1 : min(max(A.k, 1), V);
-    float tau = -INFINITY;
-    bool strict = false;
-    bool tie = false;
-    float tie_val = -INFINITY;
-    int cnt = 0;
+    // ---- stream: each wave owns its share, no workgroup barrier ----------
+    float *bv = S.cval + w * CAPW;
+    int *bi = S.cidx + w * CAPW;
+    unsigned *hist = S.u.h.whist[w];
+    WState st;
+    st.tau = -INFINITY;
+    st.strict = 0;
+    st.cnt = 0;
+    const bool bias_vec = HAS_BIAS && ((((uintptr_t)(A.bias + g.head)) & 15) == 0);
 
-    for (int t = 0; t < g.ntiles; ++t) {
-        float y[VPT + 1];
-        uint64_t m = load_tile<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, t, tau, strict, use_hash, y);
-        const int c = __popcll(m);
-        int total;
-        const int off = block_excl_scan(c, total, S.wsum[t & 1]);
-        if (cnt + total <= CAP) {
-            int pos = cnt + off;
-#pragma unroll
-            for (int i = 0; i <= VPT; ++i) {
-                if ((m >> i) & 1ull) {
-                    S.cval[pos] = y[i];
-                    S.cidx[pos] = tile_elem(g, t, i);
-                    pos++;
-                }
-            }
-            cnt += total;
-        } else {
-            // overflow: raise tau to the k-th largest of buffer + this tile
-            const uint32_t K = block_kth_key<VPT + 1>(S, cnt, y, m, k);
-            const float tk = keyf(K);
-            // entries >= tk in buffer and tile
-            float bv[PER];
-            int bi[PER];
-            int nb_ge = 0, nb_gt = 0;
-#pragma unroll
-            for (int r = 0; r < PER; ++r) {
-                const int j = tid + r * WG;
-                bv[r] = (j < cnt) ? S.cval[j] : NAN;
-                bi[r] = (j < cnt) ? S.cidx[j] : -1;
-                nb_ge += (bv[r] >= tk);
-                nb_gt += (bv[r] > tk);
-            }
-            int nt_ge = 0, nt_gt = 0;
-#pragma unroll
-            for (int i = 0; i <= VPT; ++i) {
-                if ((m >> i) & 1ull) {
-                    nt_ge += (y[i] >= tk);
-                    nt_gt += (y[i] > tk);
-                }
-            }
-            const int n_ge = block_sum(S, nb_ge + nt_ge);
-            const bool use_strict = n_ge > CAP;
-            const int mine = use_strict ? (nb_gt + nt_gt) : (nb_ge + nt_ge);
-            int tot2;
-            const int off2 = block_excl_scan(mine, tot2, S.wsum[(t + 1) & 1]);
-            __syncthreads();  // every thread has its buffer entries in registers
-            int pos = off2;
-#pragma unroll
-            for (int r = 0; r < PER; ++r) {
-                if (use_strict ? (bv[r] > tk) : (bv[r] >= tk)) {
-                    S.cval[pos] = bv[r];
-                    S.cidx[pos] = bi[r];
-                    pos++;
-                }
-            }
-#pragma unroll
-            for (int i = 0; i <= VPT; ++i) {
-                if (((m >> i) & 1ull) && (use_strict ? (y[i] > tk) : (y[i] >= tk))) {
-                    S.cval[pos] = y[i];
-                    S.cidx[pos] = tile_elem(g, t, i);
-                    pos++;
-                }
-            }
-            cnt = tot2;
-            tau = tk;
-            strict = use_strict;
-            if (use_strict) {
-                tie = true;
-                tie_val = tk;
-            }
-            __syncthreads();
+    if (w == 0 && g.head + g.ntail > 0) {
+        // head / tail elements outside the aligned body
+        const int e = extra_elem(g, lane);
+        float x[4] = {NAN, NAN, NAN, NAN};
+        const int eb[1] = {e};
+        uint32_t m = 0;
+        if (e >= 0) {
+            x[0] = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
+            m = passes(x[0], st.tau, st.strict) ? 1u : 0u;
         }
+        wave_offer<1, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, m, st, k, &S.tau_key);
+    }
+
+    for (int q0 = qb; q0 < qe; q0 += WITER) {
+        f32x4 nxt[U4];
+        const bool more = q0 + WITER < qe;
+#pragma unroll
+        for (int u = 0; u < U4; ++u) {
+            const int q = q0 + WITER + u * 64 + lane;
+            nxt[u] = (more && q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+        }
+        // effective filter: own threshold, or the largest any wave of this
+        // row has reached (each is a lower bound of the row's k-th largest)
+        const unsigned tks = *(volatile unsigned *)&S.tau_key;
+        const float tsh = tks ? keyf(tks) : -INFINITY;
+        const bool own = st.tau >= tsh;
+        const float thr = own ? st.tau : tsh;
+        const bool sx = own && st.strict;
+        float x[VPL];
+        int eb[U4];
+        uint32_t m = 0;
+#pragma unroll
+        for (int u = 0; u < U4; ++u) {
+            const int q = q0 + u * 64 + lane;
+            eb[u] = g.head + 4 * q;
+            f32x4 bb = {0.0f, 0.0f, 0.0f, 0.0f};
+            if (HAS_BIAS && bias_vec && q < qe)
+                bb = *reinterpret_cast<const f32x4 *>(A.bias + eb[u]);
+            uint32_t ab = 0xFu;
+            if (HAS_ALLOW && q < qe) {
+                const uint64_t w2 = ((uint64_t)abits[(eb[u] + 3) >> 5] << 32) | abits[eb[u] >> 5];
+                ab = (uint32_t)(w2 >> (eb[u] & 31)) & 0xFu;
+            }
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float v = cur[u][c];
+                if (HAS_BIAS) v = v + (bias_vec ? bb[c] : ((q < qe) ? A.bias[eb[u] + c] : 0.0f));
+                if (HAS_ALLOW && !((ab >> c) & 1u)) v = -INFINITY;
+                if (q >= qe) v = NAN;
+                x[4 * u + c] = v;
+                if (passes(v, thr, sx)) m |= 1u << (4 * u + c);
+            }
+        }
+        if (__ballot(m != 0u))
+            wave_offer<U4, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, m, st, k, &S.tau_key);
+#pragma unroll
+        for (int u = 0; u < U4; ++u) cur[u] = nxt[u];
+    }
+    // resolve the entries still holding upper bounds
+    if (use_hash) wave_refine(bv, bi, st.cnt, S.hkey, S.u.h.hval, -INFINITY, false);
+    int alive = 0;
+    for (int j = lane; j < st.cnt; j += 64) alive += (bv[j] == bv[j]);
+    alive = wave_sum(alive);
+    if (lane == 0) {
+        S.wcnt[w] = st.cnt;
+        S.walive[w] = alive;
+        S.wtau[w] = st.tau;
+        S.wstrict[w] = st.strict;
     }
     __syncthreads();
 
-    // ---- exact threshold ------------------------------------------------
-    float T;
+    // ---- exact threshold over the union of the wave buffers ---------------
+    int total = 0, any_strict = 0;
+    float tstar = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < NWAVE; ++ww) {
+        total += S.walive[ww];
+        if (S.wstrict[ww]) {
+            any_strict = 1;
+            tstar = fmaxf(tstar, S.wtau[ww]);
+        }
+    }
+    float T = -INFINITY;
     bool rescan = false;
-    if (cnt >= k) {
-        const float none[VPT + 1] = {};
-        const uint32_t K = block_kth_key<VPT + 1>(S, cnt, none, 0ull, k);
-        T = keyf(K);
-    } else if (tie) {
-        T = tie_val;       // fewer than k stored above the tie value
+    if (total >= k) {
+        T = keyf(block_kth_union<CAPW>(S, k));
+        if (any_strict && T <= tstar) {
+            T = tstar;
+            rescan = true;
+        }
+    } else if (any_strict) {
+        T = tstar;
         rescan = true;
-    } else {
-        T = -INFINITY;     // fewer than k non-nan values in the row
-        if (cnt == 0) rescan = true;
     }
 
     const bool top_p_on = (A.top_p > 0.0f && A.top_p < 1.0f) && !A.greedy;
-    const float u = A.uniforms ? A.uniforms[b] : 0.0f;
+    const float uu = A.uniforms ? A.uniforms[b] : 0.0f;
     int token = V - 1;
     int n_cand = 0, n_kept = 0;
     float sum2 = 0.0f;
 
+    // ---- the pool (>= T) of every wave buffer --------------------------
+    float rv[PER];
+    int ri[PER];
+    int nc = 0, off = 0;
     if (!rescan) {
-        // ---- compact candidates (>= T) to the front, then sort by id -------
-        float bv[PER];
-        int bi[PER];
         int mine = 0;
+        const int cnt_w = S.wcnt[w];
 #pragma unroll
         for (int r = 0; r < PER; ++r) {
-            const int j = tid + r * WG;
-            bv[r] = (j < cnt) ? S.cval[j] : NAN;
-            bi[r] = (j < cnt) ? S.cidx[j] : -1;
-            mine += (bv[r] >= T);
+            const int j = lane + 64 * r;  // own wave's buffer
+            rv[r] = (j < cnt_w) ? bv[j] : NAN;
+            ri[r] = (j < cnt_w) ? bi[j] : -1;
+            mine += (rv[r] >= T);
         }
-        int nc;
-        const int off = block_excl_scan(mine, nc, S.wsum[0]);
+        off = block_excl_scan(mine, nc, S.wsum[0]);
+        if (nc > EP_ALL) rescan = true;  // epilogue scratch too small: id-order rescan
+    }
+
+    if (!rescan) {
+        // ---- compact the pool to the front, then sort by id ---------------
         __syncthreads();
         int pos = off;
 #pragma unroll
         for (int r = 0; r < PER; ++r) {
-            if (bv[r] >= T) {
-                S.cval[pos] = bv[r];
-                S.cidx[pos] = bi[r];
+            if (rv[r] >= T) {
+                S.cval[pos] = rv[r];
+                S.cidx[pos] = ri[r];
                 pos++;
             }
         }
         __syncthreads();
         n_cand = nc;
-        // rank sort by id (ids are distinct)
         int rk[PER];
 #pragma unroll
         for (int r = 0; r < PER; ++r) {
             const int j = tid + r * WG;
             rk[r] = -1;
             if (j < nc) {
-                bv[r] = S.cval[j];
-                bi[r] = S.cidx[j];
+                rv[r] = S.cval[j];
+                ri[r] = S.cidx[j];
                 int rank = 0;
-                for (int q = 0; q < nc; ++q) rank += (S.cidx[q] < bi[r]);
+                for (int q = 0; q < nc; ++q) rank += (S.cidx[q] < ri[r]);
                 rk[r] = rank;
             }
         }
@@ -876,190 +1272,64 @@ __global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
 #pragma unroll
         for (int r = 0; r < PER; ++r) {
             if (rk[r] >= 0) {
-                S.cval[rk[r]] = bv[r];
-                S.cidx[rk[r]] = bi[r];
+                S.cval[rk[r]] = rv[r];
+                S.cidx[rk[r]] = ri[r];
             }
         }
         __syncthreads();
 
-        if (A.greedy) {
+        if (nc == 0) {
+            token = V - 1;
+        } else if (A.greedy) {
             token = S.cidx[0];
             n_kept = 1;
-        } else {
-            // per-entry state, entry j = tid + r*WG, in id order
-            float yv[PER];
-            bool nuc[PER], ban[PER], kept[PER];
-#pragma unroll
-            for (int r = 0; r < PER; ++r) {
-                const int j = tid + r * WG;
-                yv[r] = (j < nc) ? S.cval[j] : NAN;
-                nuc[r] = (j < nc);
-                ban[r] = false;
-                if (j < nc && A.any_bans) {
-                    const int s = hash_find(S, S.cidx[j]);
-                    ban[r] = (s >= 0) && (S.hinfo[s] & HF_BAN);
-                }
-            }
-            if (top_p_on) {
-                // gpt2_server.c:2908-2955: probabilities over the pool
-                float lm = -INFINITY;
-#pragma unroll
-                for (int r = 0; r < PER; ++r)
-                    if (tid + r * WG < nc) lm = fmaxf(lm, yv[r]);
-                float amax = block_max(S, lm);
-                if (!(amax > -1e30f)) amax = -1e30f;
-                float e1[PER];
-#pragma unroll
-                for (int r = 0; r < PER; ++r) {
-                    const int j = tid + r * WG;
-                    e1[r] = (j < nc) ? glibc_expf((yv[r] - amax) / A.T) : 0.0f;
-                    if (j < nc) S.ep[j] = e1[r];
-                }
-                const float se = block_seq_prefix(S, nc, 0.0f);
-                const float inv = 1.0f / (se + 1e-12f);
-                float pr[PER];
-#pragma unroll
-                for (int r = 0; r < PER; ++r) {
-                    const int j = tid + r * WG;
-                    pr[r] = e1[r] * inv;
-                    if (j < nc) S.ep[j] = pr[r];
-                }
-                __syncthreads();
-                // stable descending rank: larger p first, ties by id
-                int prk[PER];
-#pragma unroll
-                for (int r = 0; r < PER; ++r) {
-                    const int j = tid + r * WG;
-                    prk[r] = -1;
-                    if (j < nc) {
-                        int rank = 0;
-                        for (int q = 0; q < nc; ++q) {
-                            const float pq = S.ep[q];
-                            rank += (pq > pr[r]) || (pq == pr[r] && q < j);
-                        }
-                        prk[r] = rank;
-                    }
-                }
-                __syncthreads();
-#pragma unroll
-                for (int r = 0; r < PER; ++r)
-                    if (prk[r] >= 0) S.ep[prk[r]] = pr[r];
-                __syncthreads();
-                // inclusive cumulative cutoff in sorted order: the running
-                // sum is monotone, so the cut is the first sorted position
-                // whose prefix reaches top_p (none: keep the whole pool)
-                block_seq_prefix(S, nc, 0.0f);
-                int fc = INT_MAX;
-#pragma unroll
-                for (int r = 0; r < PER; ++r) {
-                    const int j = tid + r * WG;
-                    if (j < nc && S.ep[j] >= A.top_p) fc = min(fc, j);
-                }
-                fc = block_min(S, fc);
-                const int cut = (fc == INT_MAX) ? nc - 1 : fc;
-#pragma unroll
-                for (int r = 0; r < PER; ++r) nuc[r] = (prk[r] >= 0) && (prk[r] <= cut);
-            }
-            // bans on the nucleus, restore the top-k pool if all dropped
-            int lk = 0;
-#pragma unroll
-            for (int r = 0; r < PER; ++r) {
-                kept[r] = nuc[r] && !ban[r];
-                lk += kept[r];
-            }
-            n_kept = block_sum(S, lk);
-            if (n_kept == 0) {
-#pragma unroll
-                for (int r = 0; r < PER; ++r) kept[r] = (tid + r * WG < nc);
-                n_kept = nc;
-            }
-            // softmax over the kept set (qwen7b_server.c:275-284)
-            float lm = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < PER; ++r)
-                if (kept[r]) lm = fmaxf(lm, yv[r]);
-            const float kmax = block_max(S, lm);
-            const float mx = (kmax > -1e30f) ? kmax : -1e30f;
-            float e2[PER];
-#pragma unroll
-            for (int r = 0; r < PER; ++r) {
-                const int j = tid + r * WG;
-                e2[r] = kept[r] ? glibc_expf((yv[r] - mx) / A.T) : 0.0f;
-                if (j < nc) S.ep[j] = kept[r] ? e2[r] : -1.0f;
-            }
-            sum2 = block_seq_prefix(S, nc, 0.0f);
-            if (A.variant == LAL_GPU_VARIANT_FILTERED && sum2 <= 0.0f) {
-                // argmax over the kept set (qwen7b_server.c:285-286)
-                int cand = INT_MAX;
-#pragma unroll
-                for (int r = 0; r < PER; ++r)
-                    if (kept[r] && yv[r] == kmax && kmax > -1e30f) cand = min(cand, tid + r * WG);
-                const int j = block_min(S, cand);
-                token = (j == INT_MAX) ? 0 : S.cidx[j];
-            } else {
-                const float rr = u * sum2;
-                if ((A.flags & LAL_GPU_F_DRAW_GPT2) && rr == 0.0f) {
-                    token = 0;
-                } else {
-                    int cand = INT_MAX;
-#pragma unroll
-                    for (int r = 0; r < PER; ++r)
-                        if (kept[r] && rr <= S.ep[tid + r * WG]) cand = min(cand, tid + r * WG);
-                    const int j = block_min(S, cand);
-                    token = (j == INT_MAX) ? V - 1 : S.cidx[j];
-                }
-            }
-            // optional candidate outputs
-            if (A.cand_ld > 0) {
-#pragma unroll
-                for (int r = 0; r < PER; ++r) {
-                    const int j = tid + r * WG;
-                    if (j < nc && j < A.cand_ld) {
-                        const size_t o = (size_t)b * A.cand_ld + j;
-                        if (A.cand_ids) A.cand_ids[o] = S.cidx[j];
-                        if (A.cand_kept) A.cand_kept[o] = kept[r] ? 1 : 0;
-                        if (A.cand_probs) A.cand_probs[o] = kept[r] ? e2[r] / sum2 : 0.0f;
-                    }
-                }
-            }
-        }
-        if (A.greedy && A.cand_ld > 0) {
             for (int j = tid; j < nc && j < A.cand_ld; j += WG) {
                 const size_t o = (size_t)b * A.cand_ld + j;
                 if (A.cand_ids) A.cand_ids[o] = S.cidx[j];
                 if (A.cand_kept) A.cand_kept[o] = (j == 0);
                 if (A.cand_probs) A.cand_probs[o] = (j == 0) ? 1.0f : 0.0f;
             }
+        } else if (nc <= 64) {
+            if (w == 0) {
+                const RowResult rr = wave_epilogue(A, S, nc, uu, b);
+                token = rr.token;
+                n_kept = rr.n_kept;
+                sum2 = rr.sum;
+            }
+        } else {
+            const RowResult rr = block_epilogue<PER>(A, S, nc, uu, b);
+            token = rr.token;
+            n_kept = rr.n_kept;
+            sum2 = rr.sum;
         }
     } else {
-        // ---- rescan: the pool is larger than the LDS buffer -------------
+        // ---- rescan: the pool is larger than the LDS buffers --------------
         if (top_p_on) {
-            token = -1;  // not supported: nucleus over a pool above CAP tokens
+            token = -1;  // not supported: nucleus over a pool above the buffers
             n_cand = -1;
         } else {
-            RescanStats st = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, use_hash, T,
-                                                              A.any_bans && !A.greedy);
             bool use_ban = A.any_bans && !A.greedy;
-            if (use_ban && st.n_kept == 0) {
+            RescanStats rs = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban);
+            if (use_ban && rs.n_kept == 0) {
                 use_ban = false;  // restore the pool
-                st = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, g, use_hash, T, false);
+                rs = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false);
             }
-            n_cand = st.n_cand;
-            n_kept = st.n_kept;
+            n_cand = rs.n_cand;
+            n_kept = rs.n_kept;
             if (A.greedy) {
-                token = st.first_kept;
+                token = rs.first_kept;
                 n_kept = 1;
                 if (A.cand_ld > 0)
                     rescan_write_cands<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false, 0.0f,
                                                             1.0f, true, token, b);
             } else {
-                const float mx = (st.max_kept > -1e30f) ? st.max_kept : -1e30f;
+                const float mx = (rs.max_kept > -1e30f) ? rs.max_kept : -1e30f;
                 sum2 = rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban,
                                                               mx, false, 0.0f, nullptr);
                 if (A.variant == LAL_GPU_VARIANT_FILTERED && sum2 <= 0.0f) {
-                    token = (st.max_kept > -1e30f) ? st.first_max_kept : 0;
+                    token = (rs.max_kept > -1e30f) ? rs.first_max_kept : 0;
                 } else {
-                    const float rr = u * sum2;
+                    const float rr = uu * sum2;
                     if ((A.flags & LAL_GPU_F_DRAW_GPT2) && rr == 0.0f) {
                         token = 0;
                     } else {
@@ -1087,25 +1357,22 @@ __global__ __launch_bounds__(WG) void sample_rows_kernel(KArgs A)
     // ---- in-place penalty side effect / penalised history values --------
     if ((A.flags & LAL_GPU_F_WRITEBACK) || A.out_hvals) {
         __syncthreads();
+        float *pv = S.u.h.hval;
         for (int s = tid; s < HSLOTS; s += WG) {
             const int key = S.hkey[s];
-            if (key >= 0) S.hval[s] = penalise(row[key], S.hinfo[s] & HCOUNT_MASK, A.pen);
+            if (key >= 0) pv[s] = penalise(row[key], S.hinfo[s] & HCOUNT_MASK, A.pen);
         }
         __syncthreads();
         if (A.out_hvals) {
             for (int i = tid; i < nh; i += WG) {
                 const int t = hrow[i];
-                if (t >= 0 && t < V) {
-                    const int s = hash_find(S, t);
-                    A.out_hvals[(size_t)b * A.hist_ld + i] = S.hval[s];
-                }
+                if (t >= 0 && t < V) A.out_hvals[(size_t)b * A.hist_ld + i] = pv[hash_find(S.hkey, t)];
             }
         }
         if (A.flags & LAL_GPU_F_WRITEBACK) {
             for (int s = tid; s < HSLOTS; s += WG) {
                 const int key = S.hkey[s];
-                if (key >= 0 && (S.hinfo[s] & HCOUNT_MASK))
-                    A.logits_w[(size_t)b * A.ld + key] = S.hval[s];
+                if (key >= 0 && (S.hinfo[s] & HCOUNT_MASK)) A.logits_w[(size_t)b * A.ld + key] = pv[s];
             }
         }
     }
@@ -1498,14 +1765,19 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
 
     hipStream_t s = (hipStream_t)stream;
     const dim3 grid(batch), block(WG);
-    if (A.bias && A.allow)
-        hipLaunchKernelGGL((sample_rows_kernel<true, true>), grid, block, 0, s, A);
-    else if (A.bias)
-        hipLaunchKernelGGL((sample_rows_kernel<true, false>), grid, block, 0, s, A);
-    else if (A.allow)
-        hipLaunchKernelGGL((sample_rows_kernel<false, true>), grid, block, 0, s, A);
-    else
-        hipLaunchKernelGGL((sample_rows_kernel<false, false>), grid, block, 0, s, A);
+    const bool small = greedy || p->top_k <= K_SMALL_MAX;
+#define LAL_LAUNCH(HB, HA)                                                                   \
+    do {                                                                                     \
+        if (small)                                                                           \
+            hipLaunchKernelGGL((sample_rows_kernel<HB, HA, CAPW_SMALL>), grid, block, 0, s, A); \
+        else                                                                                 \
+            hipLaunchKernelGGL((sample_rows_kernel<HB, HA, CAPW_LARGE>), grid, block, 0, s, A); \
+    } while (0)
+    if (A.bias && A.allow) LAL_LAUNCH(true, true);
+    else if (A.bias) LAL_LAUNCH(true, false);
+    else if (A.allow) LAL_LAUNCH(false, true);
+    else LAL_LAUNCH(false, false);
+#undef LAL_LAUNCH
     LAL_HIP(hipGetLastError());
     return LAL_GPU_OK;
 }
