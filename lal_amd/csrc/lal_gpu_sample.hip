@@ -127,7 +127,8 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ int lane_id() { return threadIdx.x & 63; }
-__device__ __forceinline__ int wave_id() { return threadIdx.x >> 6; }
+// wave index as a wave-uniform (scalar) value
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Orders this wave's LDS accesses before/after the point (lanes of one wave
 // exchange data through LDS without a workgroup barrier).
@@ -344,6 +345,16 @@ __device__ __forceinline__ bool passes(float y, float tau, bool strict)
     return strict ? (y > tau) : (y >= tau);
 }
 
+// Smallest float above t (y > t  <=>  y >= next_up(t) for non-nan y); +inf
+// maps to nan so that nothing passes.
+__device__ __forceinline__ float next_up(float t)
+{
+    const uint32_t u = __float_as_uint(t);
+    if (t != t || u == 0x7f800000u) return __uint_as_float(0x7fc00000u);
+    if ((u & 0x7fffffffu) == 0) return __uint_as_float(1u);  // +-0 -> smallest denormal
+    return __uint_as_float((u & 0x80000000u) ? u - 1 : u + 1);
+}
+
 // Sequential fp32 prefix sums over ep[0..n) in index order, done by wave 0
 // (lane l of a 64-chunk receives the running sum after element base+l).  The
 // additions happen in exactly the order of the reference's scalar loop.
@@ -529,105 +540,111 @@ __device__ __forceinline__ void wave_refine(float *bv, int *bi, int cnt, const i
 // bit is set in m.  On overflow the wave refines its buffer and the offered
 // values, raises tau to the k-th largest of them and compacts.
 // Wave-synchronous, no workgroup barrier.
+__device__ __forceinline__ int lanes_below(unsigned long long mk)
+{
+    return (int)__builtin_amdgcn_mbcnt_hi((uint32_t)(mk >> 32),
+                                          __builtin_amdgcn_mbcnt_lo((uint32_t)mk, 0u));
+}
+
+// In-place compaction of bv/bi[0..cnt) keeping entries that pass (tau,
+// strict), 64 entries at a time (every lane reads its entry before any lane
+// writes, and writes never reach an entry not yet read).  Returns the count.
+__device__ __forceinline__ int wave_compact(float *bv, int *bi, int cnt, float tau, bool strict)
+{
+    int base = 0;
+    const int lane = lane_id();
+    for (int j0 = 0; j0 < cnt; j0 += 64) {
+        const int j = j0 + lane;
+        const float v = (j < cnt) ? bv[j] : NAN;
+        const int id = (j < cnt) ? bi[j] : 0;
+        const bool keep = passes(v, tau, strict);
+        const unsigned long long mk = __ballot(keep);
+        if (keep) {
+            const int pos = base + lanes_below(mk);
+            bv[pos] = v;
+            bi[pos] = id;
+        }
+        base += __popcll(mk);
+    }
+    wave_sync();
+    return base;
+}
+
+// Append the offered values x[i] (bit i of m) that pass (tau, strict).
+template <int NQ>
+__device__ __forceinline__ int wave_append(float *bv, int *bi, int base, const float (&x)[4 * NQ],
+                                           const int (&eb)[NQ], uint32_t m, float tau, bool strict,
+                                           int tag)
+{
+#pragma unroll
+    for (int i = 0; i < 4 * NQ; ++i) {
+        const bool p = ((m >> i) & 1u) && passes(x[i], tau, strict);
+        const unsigned long long mk = __ballot(p);
+        if (mk) {
+            if (p) {
+                const int pos = base + lanes_below(mk);
+                bv[pos] = x[i];
+                bi[pos] = (eb[i >> 2] + (i & 3)) | tag;
+            }
+            base += __popcll(mk);
+        }
+    }
+    return base;
+}
+
+// Offer this wave's values to its buffer: x[i] are upper bounds of the
+// processed logits (nan when out of range), tcmp the current filter.  On
+// overflow the wave resolves exact values (into a separate array), raises tau
+// to the k-th largest of buffer + offered values and compacts.
+// Wave-synchronous, no workgroup barrier.
 template <int NQ, int CAPW>
 __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, const int *hkey,
                                            const float *hval, bool use_hash, const float (&x)[4 * NQ],
-                                           const int (&eb)[NQ], uint32_t m, WState &st, int k,
+                                           const int (&eb)[NQ], float tcmp, WState &st, int k,
                                            unsigned *tau_key_shared)
 {
     constexpr int NV = 4 * NQ;
     const int tag = use_hash ? UNREFINED : 0;
-    int c = __popc(m);
-    int incl = wave_incl_scan(c);
-    int total = readlane_i(incl, 63);
+    uint32_t m = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) m |= (x[i] >= tcmp) ? (1u << i) : 0u;
+    const int total = wave_sum(__popc(m));
     if (total == 0) return;
     if (st.cnt + total <= CAPW) {
-        int pos = st.cnt + incl - c;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            if ((m >> i) & 1u) {
-                bv[pos] = x[i];
-                bi[pos] = (eb[i >> 2] + (i & 3)) | tag;
-                pos++;
-            }
-        }
-        st.cnt += total;
-        wave_sync();
+        st.cnt = wave_append<NQ>(bv, bi, st.cnt, x, eb, m, -INFINITY, false, tag);
         return;
     }
-    // overflow: exact values first
+    // overflow: exact values for the offered entries and the buffer
     float y[NV];
 #pragma unroll
     for (int i = 0; i < NV; ++i) {
         y[i] = x[i];
         if ((m >> i) & 1u) {
-            const int e = eb[i >> 2] + (i & 3);
-            y[i] = exact_value(hkey, hval, use_hash, e, x[i]);
+            y[i] = exact_value(hkey, hval, use_hash, eb[i >> 2] + (i & 3), x[i]);
             if (!passes(y[i], st.tau, st.strict)) m &= ~(1u << i);
         }
     }
     wave_sync();
     if (use_hash) wave_refine(bv, bi, st.cnt, hkey, hval, st.tau, st.strict);
-    int alive = 0;
-    for (int j = lane_id(); j < st.cnt; j += 64) alive += (bv[j] == bv[j]);
-    alive = wave_sum(alive);
-    c = __popc(m);
-    total = wave_sum(c);
-    constexpr int R = CAPW / 64;
-    float rb[R];
-    int ri[R];
-    const int lane = lane_id();
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        const int j = lane + 64 * r;
-        rb[r] = (j < st.cnt) ? bv[j] : NAN;
-        ri[r] = (j < st.cnt) ? bi[j] : -1;
-    }
+    int cnt = wave_compact(bv, bi, st.cnt, st.tau, st.strict);
+    const int offered = wave_sum(__popc(m));
     float tk = st.tau;
     bool strict = st.strict;
-    if (alive + total > CAPW) {
-        tk = keyf(wave_kth_key<NV>(hist, bv, st.cnt, y, m, k));
+    if (cnt + offered > CAPW) {
+        tk = keyf(wave_kth_key<NV>(hist, bv, cnt, y, m, k));
         int nge = 0;
+        for (int j = lane_id(); j < cnt; j += 64) nge += (bv[j] >= tk);
 #pragma unroll
-        for (int r = 0; r < R; ++r) nge += (rb[r] >= tk);
-#pragma unroll
-        for (int i = 0; i < NV; ++i)
-            if ((m >> i) & 1u) nge += (y[i] >= tk);
+        for (int i = 0; i < NV; ++i) nge += ((m >> i) & 1u) && (y[i] >= tk);
         strict = wave_sum(nge) > CAPW;
+        cnt = wave_compact(bv, bi, cnt, tk, strict);
     }
-    // keep buffer entries and offered values that pass (tk, strict)
-    int mine = 0;
-#pragma unroll
-    for (int r = 0; r < R; ++r) mine += passes(rb[r], tk, strict);
-#pragma unroll
-    for (int i = 0; i < NV; ++i)
-        if ((m >> i) & 1u) mine += passes(y[i], tk, strict);
-    const int incl2 = wave_incl_scan(mine);
-    const int tot2 = readlane_i(incl2, 63);
-    int pos = incl2 - mine;
-    wave_sync();  // every lane holds its buffer entries in registers
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-        if (passes(rb[r], tk, strict)) {
-            bv[pos] = rb[r];
-            bi[pos] = ri[r];
-            pos++;
-        }
-    }
-#pragma unroll
-    for (int i = 0; i < NV; ++i) {
-        if (((m >> i) & 1u) && passes(y[i], tk, strict)) {
-            bv[pos] = y[i];
-            bi[pos] = eb[i >> 2] + (i & 3);
-            pos++;
-        }
-    }
+    st.cnt = wave_append<NQ>(bv, bi, cnt, y, eb, m, tk, strict, 0);
     wave_sync();
-    st.cnt = tot2;
     if (tk != st.tau || strict != (bool)st.strict) {
         st.tau = tk;
         st.strict = strict ? 1 : 0;
-        if (lane == 0) atomicMax(tau_key_shared, fkey(tk));
+        if (lane_id() == 0) atomicMax(tau_key_shared, fkey(tk));
     }
 }
 
@@ -1127,56 +1144,80 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const int e = extra_elem(g, lane);
         float x[4] = {NAN, NAN, NAN, NAN};
         const int eb[1] = {e};
-        uint32_t m = 0;
-        if (e >= 0) {
-            x[0] = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
-            m = passes(x[0], st.tau, st.strict) ? 1u : 0u;
-        }
-        wave_offer<1, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, m, st, k, &S.tau_key);
+        if (e >= 0) x[0] = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
+        wave_offer<1, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, -INFINITY, st, k,
+                            &S.tau_key);
     }
 
     for (int q0 = qb; q0 < qe; q0 += WITER) {
         f32x4 nxt[U4];
-        const bool more = q0 + WITER < qe;
+        if (q0 + 2 * WITER <= qe) {
+            // next iteration lies fully inside this wave's share
 #pragma unroll
-        for (int u = 0; u < U4; ++u) {
-            const int q = q0 + WITER + u * 64 + lane;
-            nxt[u] = (more && q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+            for (int u = 0; u < U4; ++u)
+                nxt[u] = __builtin_nontemporal_load(row4 + q0 + WITER + u * 64 + lane);
+        } else {
+#pragma unroll
+            for (int u = 0; u < U4; ++u) {
+                const int q = q0 + WITER + u * 64 + lane;
+                nxt[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+            }
         }
         // effective filter: own threshold, or the largest any wave of this
-        // row has reached (each is a lower bound of the row's k-th largest)
-        const unsigned tks = *(volatile unsigned *)&S.tau_key;
+        // row has reached (each is a lower bound of the row's k-th largest);
+        // a strict threshold becomes ">=" against the next float up
+        const unsigned tks = S.tau_key;
         const float tsh = tks ? keyf(tks) : -INFINITY;
         const bool own = st.tau >= tsh;
         const float thr = own ? st.tau : tsh;
         const bool sx = own && st.strict;
+        const float tcmp = sx ? next_up(thr) : thr;
+        // processed-value upper bounds (values of invalid lanes are nan)
         float x[VPL];
-        int eb[U4];
-        uint32_t m = 0;
 #pragma unroll
         for (int u = 0; u < U4; ++u) {
-            const int q = q0 + u * 64 + lane;
-            eb[u] = g.head + 4 * q;
+            const int e0 = g.head + 4 * (q0 + u * 64 + lane);
             f32x4 bb = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (HAS_BIAS && bias_vec && q < qe)
-                bb = *reinterpret_cast<const f32x4 *>(A.bias + eb[u]);
+            if (HAS_BIAS) {
+                if (bias_vec) {
+                    bb = *reinterpret_cast<const f32x4 *>(A.bias + min(e0, V - 4));
+                } else {
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) bb[c] = A.bias[min(e0 + c, V - 1)];
+                }
+            }
             uint32_t ab = 0xFu;
-            if (HAS_ALLOW && q < qe) {
-                const uint64_t w2 = ((uint64_t)abits[(eb[u] + 3) >> 5] << 32) | abits[eb[u] >> 5];
-                ab = (uint32_t)(w2 >> (eb[u] & 31)) & 0xFu;
+            if (HAS_ALLOW) {
+                const int ea = min(e0, V - 4 >= 0 ? V - 4 : 0);
+                const uint64_t w2 = ((uint64_t)abits[min(ea + 3, V - 1) >> 5] << 32) | abits[ea >> 5];
+                ab = (uint32_t)(w2 >> (ea & 31)) & 0xFu;
             }
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 float v = cur[u][c];
-                if (HAS_BIAS) v = v + (bias_vec ? bb[c] : ((q < qe) ? A.bias[eb[u] + c] : 0.0f));
+                if (HAS_BIAS) v = v + bb[c];
                 if (HAS_ALLOW && !((ab >> c) & 1u)) v = -INFINITY;
-                if (q >= qe) v = NAN;
                 x[4 * u + c] = v;
-                if (passes(v, thr, sx)) m |= 1u << (4 * u + c);
             }
         }
-        if (__ballot(m != 0u))
-            wave_offer<U4, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, m, st, k, &S.tau_key);
+        if ((HAS_BIAS || HAS_ALLOW) && q0 + WITER > qe) {
+            // partial last iteration: lanes past the share stay out
+#pragma unroll
+            for (int u = 0; u < U4; ++u)
+                if (q0 + u * 64 + lane >= qe)
+#pragma unroll
+                    for (int c = 0; c < 4; ++c) x[4 * u + c] = NAN;
+        }
+        unsigned long long any = 0ull;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) any |= __ballot(x[i] >= tcmp);
+        if (any) {
+            int eb[U4];
+#pragma unroll
+            for (int u = 0; u < U4; ++u) eb[u] = g.head + 4 * (q0 + u * 64 + lane);
+            wave_offer<U4, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, tcmp, st, k,
+                                 &S.tau_key);
+        }
 #pragma unroll
         for (int u = 0; u < U4; ++u) cur[u] = nxt[u];
     }
