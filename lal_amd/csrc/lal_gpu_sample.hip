@@ -454,6 +454,27 @@ __device__ __forceinline__ float exact_value(const int *hkey, const float *hval,
     return yhat;
 }
 
+// k-th largest (1-based, k <= 64) of one value per lane, by a register
+// bitonic sort across the wave (descending; nan sorts last).
+__device__ __forceinline__ float wave_kth_of_lanes(float v, int k)
+{
+    const int lane = lane_id();
+    uint32_t key = (v == v) ? fkey(v) : 0u;
+#pragma unroll
+    for (int size = 2; size <= 64; size <<= 1) {
+#pragma unroll
+        for (int stride = size >> 1; stride > 0; stride >>= 1) {
+            const uint32_t other = (uint32_t)__shfl_xor((int)key, stride, 64);
+            const bool up = ((lane & size) == 0);          // this run sorts descending
+            const bool lower = ((lane & stride) == 0);
+            const bool take_max = (up == lower);
+            key = take_max ? max(key, other) : min(key, other);
+        }
+    }
+    const uint32_t kk = (uint32_t)readlane_i((int)key, k - 1);
+    return kk ? keyf(kk) : -INFINITY;
+}
+
 // ---------------------------------------------------------------------------
 // Per-wave state and candidate buffer
 // ---------------------------------------------------------------------------
@@ -1086,12 +1107,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     const int qe = (int)(((long long)g.nb4 * (w + 1)) / NWAVE);
     const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
 
-    // first iteration's loads go out before the hash setup
-    f32x4 cur[U4];
+    // the first two iterations' loads go out before the hash setup
+    f32x4 cur[U4], nx1[U4];
 #pragma unroll
     for (int u = 0; u < U4; ++u) {
         const int q = qb + u * 64 + lane;
         cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+        const int q1 = qb + WITER + u * 64 + lane;
+        nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
     }
 
     // ---- setup: hash of history / ban ids -------------------------------
@@ -1150,17 +1173,17 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
 
     for (int q0 = qb; q0 < qe; q0 += WITER) {
-        f32x4 nxt[U4];
-        if (q0 + 2 * WITER <= qe) {
-            // next iteration lies fully inside this wave's share
+        // two iterations stay in flight while this one is filtered
+        f32x4 nx2[U4];
+        if (q0 + 3 * WITER <= qe) {
 #pragma unroll
             for (int u = 0; u < U4; ++u)
-                nxt[u] = __builtin_nontemporal_load(row4 + q0 + WITER + u * 64 + lane);
+                nx2[u] = __builtin_nontemporal_load(row4 + q0 + 2 * WITER + u * 64 + lane);
         } else {
 #pragma unroll
             for (int u = 0; u < U4; ++u) {
-                const int q = q0 + WITER + u * 64 + lane;
-                nxt[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+                const int q = q0 + 2 * WITER + u * 64 + lane;
+                nx2[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
             }
         }
         // effective filter: own threshold, or the largest any wave of this
@@ -1171,7 +1194,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const bool own = st.tau >= tsh;
         const float thr = own ? st.tau : tsh;
         const bool sx = own && st.strict;
-        const float tcmp = sx ? next_up(thr) : thr;
+        float tcmp = sx ? next_up(thr) : thr;
         // processed-value upper bounds (values of invalid lanes are nan)
         float x[VPL];
 #pragma unroll
@@ -1208,6 +1231,28 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 #pragma unroll
                     for (int c = 0; c < 4; ++c) x[4 * u + c] = NAN;
         }
+        if (q0 == qb && k <= 64 && st.tau == -INFINITY) {
+            // initial bound: the k-th largest of the 64 per-lane maxima of this
+            // first iteration (a subset's k-th largest never exceeds the row's)
+            // exact value of each lane's largest upper bound (one hash lookup)
+            float lm = x[0];
+            int li = 0;
+#pragma unroll
+            for (int i = 1; i < VPL; ++i)
+                if (x[i] > lm) {
+                    lm = x[i];
+                    li = i;
+                }
+            if (use_hash && lm == lm)
+                lm = exact_value(S.hkey, S.u.h.hval, true, g.head + 4 * (q0 + (li >> 2) * 64 + lane) + (li & 3),
+                                 lm);
+            const float t0 = wave_kth_of_lanes(lm, k);
+            if (t0 > -INFINITY) {
+                st.tau = t0;
+                if (lane == 0) atomicMax(&S.tau_key, fkey(t0));
+            }
+            tcmp = fmaxf(tcmp, st.tau);
+        }
         unsigned long long any = 0ull;
 #pragma unroll
         for (int i = 0; i < VPL; ++i) any |= __ballot(x[i] >= tcmp);
@@ -1219,7 +1264,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
                                  &S.tau_key);
         }
 #pragma unroll
-        for (int u = 0; u < U4; ++u) cur[u] = nxt[u];
+        for (int u = 0; u < U4; ++u) {
+            cur[u] = nx1[u];
+            nx1[u] = nx2[u];
+        }
     }
     // resolve the entries still holding upper bounds
     if (use_hash) wave_refine(bv, bi, st.cnt, S.hkey, S.u.h.hval, -INFINITY, false);
