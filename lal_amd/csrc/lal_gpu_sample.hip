@@ -56,6 +56,9 @@ constexpr int RS_CHUNK = NWAVE * 256;         // rescan chunk (lives in the hist
 constexpr int CAPW_SMALL = 512;
 constexpr int CAPW_LARGE = 2048;
 constexpr int K_SMALL_MAX = 128;
+// row sample for the threshold estimate: 64 float4 (1 KB) every SBLK float4
+constexpr int SBLK = 2048;          // 32 KB stride -> 1/32 of the row
+constexpr int SR = 5;               // float4 per thread: up to 20 sampled blocks (V <= 163840 fully sampled)
 
 static_assert(2 * HSLOTS >= 3 * (LAL_GPU_MAX_HISTORY + LAL_GPU_MAX_BAN_IDS), "hash load <= 2/3");
 static_assert(CAPW_SMALL > K_SMALL_MAX && CAPW_LARGE > LAL_GPU_MAX_K, "buffer above k");
@@ -717,6 +720,53 @@ __device__ __forceinline__ uint32_t block_kth_union(SM &S, int k)
     return prefix;
 }
 
+// Block radix select: k-th largest key over the register values v[i] of all
+// threads whose bit is set in m.  Requires >= k inputs.
+template <int NV, class SM>
+__device__ __forceinline__ uint32_t block_kth_regs(SM &S, const float (&v)[NV], uint32_t m, int k)
+{
+    unsigned *hist = S.u.h.whist[0];
+    uint32_t prefix = 0, pmask = 0;
+    int rem = k;
+    for (int pass = 0; pass < 4; ++pass) {
+        const int shift = 24 - 8 * pass;
+        __syncthreads();
+        hist[threadIdx.x] = 0;
+        __syncthreads();
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            if ((m >> i) & 1u) {
+                const uint32_t key = fkey(v[i]);
+                if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+            }
+        }
+        __syncthreads();
+        if (wave_id() == 0) {
+            const int lane = lane_id();
+            const int b0 = 255 - 4 * lane;
+            const int h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
+            const int lsum = h0 + h1 + h2 + h3;
+            const int incl = wave_incl_scan(lsum);
+            const int excl = incl - lsum;
+            if (excl < rem && rem <= incl) {
+                int r = rem - excl, d;
+                if (r <= h0) d = b0;
+                else if ((r -= h0) <= h1) d = b0 - 1;
+                else if ((r -= h1) <= h2) d = b0 - 2;
+                else { r -= h2; d = b0 - 3; }
+                S.sel_digit = d;
+                S.sel_rem = r;
+            }
+        }
+        __syncthreads();
+        prefix |= (uint32_t)S.sel_digit << shift;
+        pmask |= 0xFFu << shift;
+        rem = S.sel_rem;
+    }
+    __syncthreads();
+    return prefix;
+}
+
 // ---------------------------------------------------------------------------
 // Rescan path: finish the row by re-reading it in id order (used when more
 // tokens tie at the threshold than the buffers hold).
@@ -1107,7 +1157,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     const int qe = (int)(((long long)g.nb4 * (w + 1)) / NWAVE);
     const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
 
-    // the first two iterations' loads go out before the hash setup
+    // the first two iterations' loads and the row sample go out before the
+    // hash setup
     f32x4 cur[U4], nx1[U4];
 #pragma unroll
     for (int u = 0; u < U4; ++u) {
@@ -1116,13 +1167,19 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const int q1 = qb + WITER + u * 64 + lane;
         nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
     }
+    f32x4 smp[SR];
+#pragma unroll
+    for (int r = 0; r < SR; ++r) {
+        const int sidx = tid + WG * r;
+        const int q = (sidx >> 6) * SBLK + (sidx & 63);
+        smp[r] = (q < g.nb4) ? row4[q] : f32x4{NAN, NAN, NAN, NAN};
+    }
 
     // ---- setup: hash of history / ban ids -------------------------------
     for (int s = tid; s < HSLOTS; s += WG) {
         S.hkey[s] = -1;
         S.hinfo[s] = 0;
     }
-    if (tid == 0) S.tau_key = 0u;  // below every real key
     __syncthreads();
     for (int i = tid; i < nh; i += WG) {
         const int t = hrow[i];
@@ -1152,16 +1209,64 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
     const bool use_hash = block_sum(S, nocc) > 0;
 
-    // ---- stream: each wave owns its share, no workgroup barrier ----------
+    // ---- threshold estimate from the sample ------------------------------
+    // tau_est = the ks-th largest exact sampled value, ks chosen so that
+    // (for any arrangement of the row's top-k among the sampled blocks with
+    // the sampling fraction f) P(tau_est above the row's k-th largest) is
+    // negligible; it is verified after streaming (>= k captured values), and
+    // the row is streamed again without it when the check fails.
+    float tau_est = -INFINITY;
+    {
+        float sv[4 * SR];
+        uint32_t sm = 0;
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+            const int sidx = tid + WG * r;
+            const int q = (sidx >> 6) * SBLK + (sidx & 63);
+#pragma unroll
+            for (int c = 0; c < 4; ++c) {
+                float v = smp[r][c];
+                if (q < g.nb4) {
+                    const int e = g.head + 4 * q + c;
+                    v = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, v);
+                    v = exact_value(S.hkey, S.u.h.hval, use_hash, e, v);
+                    if (v == v) sm |= 1u << (4 * r + c);
+                }
+                sv[4 * r + c] = v;
+            }
+        }
+        const int nsmp = block_sum(S, __popc(sm));
+        if (nsmp > 0 && !A.greedy) {
+            const float lam = (float)k * (float)nsmp / (float)V;
+            const int ks = (int)ceilf(lam + 6.0f * sqrtf(lam) + 6.0f);
+            if (ks <= nsmp && ks < k * 4 + 64) tau_est = keyf(block_kth_regs<4 * SR>(S, sv, sm, ks));
+        }
+    }
+
     float *bv = S.cval + w * CAPW;
     int *bi = S.cidx + w * CAPW;
     unsigned *hist = S.u.h.whist[w];
-    WState st;
-    st.tau = -INFINITY;
-    st.strict = 0;
-    st.cnt = 0;
     const bool bias_vec = HAS_BIAS && ((((uintptr_t)(A.bias + g.head)) & 15) == 0);
+    WState st;
+    for (int attempt = 0; attempt < 2; ++attempt) {
+        if (attempt == 1) {
+            // the estimate was above the row's k-th largest: stream again
+#pragma unroll
+            for (int u = 0; u < U4; ++u) {
+                const int q = qb + u * 64 + lane;
+                cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+                const int q1 = qb + WITER + u * 64 + lane;
+                nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
+            }
+        }
+        __syncthreads();
+        if (tid == 0) S.tau_key = (tau_est > -INFINITY) ? fkey(tau_est) : 0u;
+        __syncthreads();
+        st.tau = -INFINITY;
+        st.strict = 0;
+        st.cnt = 0;
 
+    // ---- stream: each wave owns its share, no workgroup barrier ----------
     if (w == 0 && g.head + g.ntail > 0) {
         // head / tail elements outside the aligned body
         const int e = extra_elem(g, lane);
@@ -1171,7 +1276,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         wave_offer<1, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, -INFINITY, st, k,
                             &S.tau_key);
     }
-
     for (int q0 = qb; q0 < qe; q0 += WITER) {
         // two iterations stay in flight while this one is filtered
         f32x4 nx2[U4];
@@ -1194,7 +1298,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const bool own = st.tau >= tsh;
         const float thr = own ? st.tau : tsh;
         const bool sx = own && st.strict;
-        float tcmp = sx ? next_up(thr) : thr;
+        const float tcmp = sx ? next_up(thr) : thr;
         // processed-value upper bounds (values of invalid lanes are nan)
         float x[VPL];
 #pragma unroll
@@ -1231,28 +1335,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 #pragma unroll
                     for (int c = 0; c < 4; ++c) x[4 * u + c] = NAN;
         }
-        if (q0 == qb && k <= 64 && st.tau == -INFINITY) {
-            // initial bound: the k-th largest of the 64 per-lane maxima of this
-            // first iteration (a subset's k-th largest never exceeds the row's)
-            // exact value of each lane's largest upper bound (one hash lookup)
-            float lm = x[0];
-            int li = 0;
-#pragma unroll
-            for (int i = 1; i < VPL; ++i)
-                if (x[i] > lm) {
-                    lm = x[i];
-                    li = i;
-                }
-            if (use_hash && lm == lm)
-                lm = exact_value(S.hkey, S.u.h.hval, true, g.head + 4 * (q0 + (li >> 2) * 64 + lane) + (li & 3),
-                                 lm);
-            const float t0 = wave_kth_of_lanes(lm, k);
-            if (t0 > -INFINITY) {
-                st.tau = t0;
-                if (lane == 0) atomicMax(&S.tau_key, fkey(t0));
-            }
-            tcmp = fmaxf(tcmp, st.tau);
-        }
         unsigned long long any = 0ull;
 #pragma unroll
         for (int i = 0; i < VPL; ++i) any |= __ballot(x[i] >= tcmp);
@@ -1269,10 +1351,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             nx1[u] = nx2[u];
         }
     }
-    // resolve the entries still holding upper bounds
-    if (use_hash) wave_refine(bv, bi, st.cnt, S.hkey, S.u.h.hval, -INFINITY, false);
+    // resolve the entries still holding upper bounds (below the estimate:
+    // dropped, so the count below verifies it)
+    if (use_hash) wave_refine(bv, bi, st.cnt, S.hkey, S.u.h.hval, tau_est, false);
     int alive = 0;
-    for (int j = lane; j < st.cnt; j += 64) alive += (bv[j] == bv[j]);
+    for (int j = lane; j < st.cnt; j += 64) alive += (bv[j] >= tau_est);
     alive = wave_sum(alive);
     if (lane == 0) {
         S.wcnt[w] = st.cnt;
@@ -1281,6 +1364,17 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         S.wstrict[w] = st.strict;
     }
     __syncthreads();
+    {
+        int tot = 0, strict_any = 0;
+#pragma unroll
+        for (int ww = 0; ww < NWAVE; ++ww) {
+            tot += S.walive[ww];
+            strict_any |= S.wstrict[ww];
+        }
+        if (tau_est == -INFINITY || strict_any || tot >= k) break;
+        tau_est = -INFINITY;
+    }
+    }  // attempt
 
     // ---- exact threshold over the union of the wave buffers ---------------
     int total = 0, any_strict = 0;
