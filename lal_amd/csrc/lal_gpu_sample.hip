@@ -446,36 +446,63 @@ __device__ __forceinline__ float upper_bound(const float *bias, const uint32_t *
     return y;
 }
 
-// exact processed value for a value that passed the upper-bound filter
-__device__ __forceinline__ float exact_value(const int *hkey, const float *hval, bool use_hash, int e,
-                                             float yhat)
+// Exact processed value of token e given its upper bound yhat: ids in the
+// hash are recomputed from the raw logit (penalty applied `count` times, then
+// bias, allow mask and the pre-selection ban); all others equal the bound.
+struct RowCtx {
+    const float *row;
+    const float *bias;
+    const uint32_t *abits;
+    const int *hkey;
+    const int *hinfo;
+    float pen;
+    bool has_bias, has_allow, use_hash;
+};
+
+__device__ __forceinline__ float exact_value(const RowCtx &R, int e, float yhat)
 {
-    if (use_hash) {
-        const int s = hash_find(hkey, e);
-        if (s >= 0) return hval[s];
+    if (R.use_hash) {
+        const int s = hash_find(R.hkey, e);
+        if (s >= 0) {
+            const int info = R.hinfo[s];
+            float y = penalise(R.row[e], info & HCOUNT_MASK, R.pen);
+            if (R.has_bias) y = y + R.bias[e];
+            if (R.has_allow && !allow_bit(R.abits, e)) y = -INFINITY;
+            if (info & HF_MASKPRE) y = -INFINITY;
+            return y;
+        }
     }
     return yhat;
 }
 
-// k-th largest (1-based, k <= 64) of one value per lane, by a register
-// bitonic sort across the wave (descending; nan sorts last).
-__device__ __forceinline__ float wave_kth_of_lanes(float v, int k)
+// Sort one key per lane descending (bitonic network over the wave).
+__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t key)
 {
     const int lane = lane_id();
-    uint32_t key = (v == v) ? fkey(v) : 0u;
 #pragma unroll
     for (int size = 2; size <= 64; size <<= 1) {
 #pragma unroll
         for (int stride = size >> 1; stride > 0; stride >>= 1) {
             const uint32_t other = (uint32_t)__shfl_xor((int)key, stride, 64);
-            const bool up = ((lane & size) == 0);          // this run sorts descending
-            const bool lower = ((lane & stride) == 0);
-            const bool take_max = (up == lower);
+            const bool take_max = (((lane & size) == 0) == ((lane & stride) == 0));
             key = take_max ? max(key, other) : min(key, other);
         }
     }
-    const uint32_t kk = (uint32_t)readlane_i((int)key, k - 1);
-    return kk ? keyf(kk) : -INFINITY;
+    return key;
+}
+
+// Top 64 of two descending-sorted lane vectors a, b, sorted descending:
+// max(a_i, b_{63-i}) is bitonic, a half-cleaner cascade sorts it.
+__device__ __forceinline__ uint32_t wave_merge_top_desc(uint32_t a, uint32_t b)
+{
+    const int lane = lane_id();
+    uint32_t key = max(a, (uint32_t)__shfl((int)b, 63 - lane, 64));
+#pragma unroll
+    for (int stride = 32; stride > 0; stride >>= 1) {
+        const uint32_t other = (uint32_t)__shfl_xor((int)key, stride, 64);
+        key = ((lane & stride) == 0) ? max(key, other) : min(key, other);
+    }
+    return key;
 }
 
 // ---------------------------------------------------------------------------
@@ -546,14 +573,14 @@ __device__ __forceinline__ uint32_t wave_kth_key(unsigned *hist, const float *bv
 // entry that fails the current threshold becomes dead (value nan).
 constexpr int UNREFINED = (int)0x80000000;
 
-__device__ __forceinline__ void wave_refine(float *bv, int *bi, int cnt, const int *hkey,
-                                            const float *hval, float tau, bool strict)
+__device__ __forceinline__ void wave_refine(float *bv, int *bi, int cnt, const RowCtx &R, float tau,
+                                            bool strict)
 {
     for (int j = lane_id(); j < cnt; j += 64) {
         const int id = bi[j];
         if (!(id & UNREFINED)) continue;
         const int e = id & ~UNREFINED;
-        const float y = exact_value(hkey, hval, true, e, bv[j]);
+        const float y = exact_value(R, e, bv[j]);
         bv[j] = passes(y, tau, strict) ? y : NAN;
         bi[j] = e;
     }
@@ -622,13 +649,13 @@ __device__ __forceinline__ int wave_append(float *bv, int *bi, int base, const f
 // to the k-th largest of buffer + offered values and compacts.
 // Wave-synchronous, no workgroup barrier.
 template <int NQ, int CAPW>
-__device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, const int *hkey,
-                                           const float *hval, bool use_hash, const float (&x)[4 * NQ],
+__device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, const RowCtx &R,
+                                           const float (&x)[4 * NQ],
                                            const int (&eb)[NQ], float tcmp, WState &st, int k,
                                            unsigned *tau_key_shared)
 {
     constexpr int NV = 4 * NQ;
-    const int tag = use_hash ? UNREFINED : 0;
+    const int tag = R.use_hash ? UNREFINED : 0;
     uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) m |= (x[i] >= tcmp) ? (1u << i) : 0u;
@@ -644,12 +671,12 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
     for (int i = 0; i < NV; ++i) {
         y[i] = x[i];
         if ((m >> i) & 1u) {
-            y[i] = exact_value(hkey, hval, use_hash, eb[i >> 2] + (i & 3), x[i]);
+            y[i] = exact_value(R, eb[i >> 2] + (i & 3), x[i]);
             if (!passes(y[i], st.tau, st.strict)) m &= ~(1u << i);
         }
     }
     wave_sync();
-    if (use_hash) wave_refine(bv, bi, st.cnt, hkey, hval, st.tau, st.strict);
+    if (R.use_hash) wave_refine(bv, bi, st.cnt, R, st.tau, st.strict);
     int cnt = wave_compact(bv, bi, st.cnt, st.tau, st.strict);
     const int offered = wave_sum(__popc(m));
     float tk = st.tau;
@@ -776,7 +803,17 @@ __device__ __forceinline__ float rescan_value(const KArgs &A, const SM &S, const
                                               const uint32_t *abits, bool use_hash, int e)
 {
     const float yh = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
-    return exact_value(S.hkey, S.u.h.hval, use_hash, e, yh);
+    RowCtx R;
+    R.row = row;
+    R.bias = A.bias;
+    R.abits = abits;
+    R.hkey = S.hkey;
+    R.hinfo = S.hinfo;
+    R.pen = A.pen;
+    R.has_bias = HAS_BIAS;
+    R.has_allow = HAS_ALLOW;
+    R.use_hash = use_hash;
+    return exact_value(R, e, yh);
 }
 
 template <class SM>
@@ -1196,50 +1233,62 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
     __syncthreads();
     int nocc = 0;
-    for (int s = tid; s < HSLOTS; s += WG) {
-        const int key = S.hkey[s];
-        if (key < 0) continue;
-        nocc++;
-        const int info = S.hinfo[s];
-        float yv = penalise(row[key], info & HCOUNT_MASK, A.pen);
-        if (HAS_BIAS) yv = yv + A.bias[key];
-        if (HAS_ALLOW && !allow_bit(abits, key)) yv = -INFINITY;
-        if (info & HF_MASKPRE) yv = -INFINITY;
-        S.u.h.hval[s] = yv;
-    }
+    for (int s = tid; s < HSLOTS; s += WG) nocc += (S.hkey[s] >= 0);
     const bool use_hash = block_sum(S, nocc) > 0;
+    RowCtx R;
+    R.row = row;
+    R.bias = A.bias;
+    R.abits = abits;
+    R.hkey = S.hkey;
+    R.hinfo = S.hinfo;
+    R.pen = A.pen;
+    R.has_bias = HAS_BIAS;
+    R.has_allow = HAS_ALLOW;
+    R.use_hash = use_hash;
 
     // ---- threshold estimate from the sample ------------------------------
-    // tau_est = the ks-th largest exact sampled value, ks chosen so that
-    // (for any arrangement of the row's top-k among the sampled blocks with
-    // the sampling fraction f) P(tau_est above the row's k-th largest) is
-    // negligible; it is verified after streaming (>= k captured values), and
+    // tau_est = the ks-th largest of the per-thread maxima of the sampled
+    // upper bounds (a subset of the sample, so no larger than the sample's
+    // ks-th largest); ks is chosen so that with the sampling fraction f the
+    // sample holds fewer than ks of the row's top-k except with negligible
+    // probability.  It is verified after streaming (>= k captured values) and
     // the row is streamed again without it when the check fails.
     float tau_est = -INFINITY;
     {
-        float sv[4 * SR];
-        uint32_t sm = 0;
+        float lm = -INFINITY;
+        int nvalid = 0;
 #pragma unroll
         for (int r = 0; r < SR; ++r) {
             const int sidx = tid + WG * r;
             const int q = (sidx >> 6) * SBLK + (sidx & 63);
+            if (q < g.nb4) {
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                float v = smp[r][c];
-                if (q < g.nb4) {
-                    const int e = g.head + 4 * q + c;
-                    v = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, v);
-                    v = exact_value(S.hkey, S.u.h.hval, use_hash, e, v);
-                    if (v == v) sm |= 1u << (4 * r + c);
+                for (int c = 0; c < 4; ++c) {
+                    const float v = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, g.head + 4 * q + c,
+                                                                     smp[r][c]);
+                    lm = fmaxf(lm, v);
+                    nvalid++;
                 }
-                sv[4 * r + c] = v;
             }
         }
-        const int nsmp = block_sum(S, __popc(sm));
-        if (nsmp > 0 && !A.greedy) {
-            const float lam = (float)k * (float)nsmp / (float)V;
-            const int ks = (int)ceilf(lam + 6.0f * sqrtf(lam) + 6.0f);
-            if (ks <= nsmp && ks < k * 4 + 64) tau_est = keyf(block_kth_regs<4 * SR>(S, sv, sm, ks));
+        const int nsmp = block_sum(S, nvalid);
+        const float lam = (float)k * (float)nsmp / (float)V;
+        const int ks = (int)ceilf(lam + 6.0f * sqrtf(lam) + 6.0f);
+        if (!A.greedy && nsmp > 0 && ks <= 64) {
+            unsigned *tmp = S.u.h.whist[0];  // 4 x 64 keys
+            const uint32_t key = wave_sort_desc((lm == lm && lm > -INFINITY) ? fkey(lm) : 0u);
+            tmp[w * 64 + lane] = key;
+            __syncthreads();
+            if (w == 0) {
+                const uint32_t a = wave_merge_top_desc(tmp[lane], tmp[64 + lane]);
+                const uint32_t c2 = wave_merge_top_desc(tmp[128 + lane], tmp[192 + lane]);
+                const uint32_t top = wave_merge_top_desc(a, c2);
+                const uint32_t kk = (uint32_t)readlane_i((int)top, ks - 1);
+                if (lane == 0) S.sel_rem = (int)kk;
+            }
+            __syncthreads();
+            const uint32_t kk = (uint32_t)S.sel_rem;
+            if (kk) tau_est = keyf(kk);
         }
     }
 
@@ -1273,8 +1322,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         float x[4] = {NAN, NAN, NAN, NAN};
         const int eb[1] = {e};
         if (e >= 0) x[0] = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
-        wave_offer<1, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, -INFINITY, st, k,
-                            &S.tau_key);
+        wave_offer<1, CAPW>(bv, bi, hist, R, x, eb, -INFINITY, st, k, &S.tau_key);
     }
     for (int q0 = qb; q0 < qe; q0 += WITER) {
         // two iterations stay in flight while this one is filtered
@@ -1342,8 +1390,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             int eb[U4];
 #pragma unroll
             for (int u = 0; u < U4; ++u) eb[u] = g.head + 4 * (q0 + u * 64 + lane);
-            wave_offer<U4, CAPW>(bv, bi, hist, S.hkey, S.u.h.hval, use_hash, x, eb, tcmp, st, k,
-                                 &S.tau_key);
+            wave_offer<U4, CAPW>(bv, bi, hist, R, x, eb, tcmp, st, k, &S.tau_key);
         }
 #pragma unroll
         for (int u = 0; u < U4; ++u) {
@@ -1353,7 +1400,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
     // resolve the entries still holding upper bounds (below the estimate:
     // dropped, so the count below verifies it)
-    if (use_hash) wave_refine(bv, bi, st.cnt, S.hkey, S.u.h.hval, tau_est, false);
+    if (use_hash) wave_refine(bv, bi, st.cnt, R, tau_est, false);
     int alive = 0;
     for (int j = lane; j < st.cnt; j += 64) alive += (bv[j] >= tau_est);
     alive = wave_sum(alive);
