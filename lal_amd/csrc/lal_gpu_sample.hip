@@ -656,15 +656,32 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
 {
     constexpr int NV = 4 * NQ;
     const int tag = R.use_hash ? UNREFINED : 0;
+    // append path: the per-slot ballots give the count (scalar popcounts) and
+    // each lane's position (mbcnt); no cross-lane data exchange
+    int total = 0;
+#pragma unroll
+    for (int i = 0; i < NV; ++i) total += __popcll(__ballot(x[i] >= tcmp));
+    if (total == 0) return;
+    if (st.cnt + total <= CAPW) {
+        int base = st.cnt;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const unsigned long long mk = __ballot(x[i] >= tcmp);
+            if (mk) {
+                if (x[i] >= tcmp) {
+                    const int pos = base + lanes_below(mk);
+                    bv[pos] = x[i];
+                    bi[pos] = (eb[i >> 2] + (i & 3)) | tag;
+                }
+                base += __popcll(mk);
+            }
+        }
+        st.cnt = base;
+        return;
+    }
     uint32_t m = 0;
 #pragma unroll
     for (int i = 0; i < NV; ++i) m |= (x[i] >= tcmp) ? (1u << i) : 0u;
-    const int total = wave_sum(__popc(m));
-    if (total == 0) return;
-    if (st.cnt + total <= CAPW) {
-        st.cnt = wave_append<NQ>(bv, bi, st.cnt, x, eb, m, -INFINITY, false, tag);
-        return;
-    }
     // overflow: exact values for the offered entries and the buffer
     float y[NV];
 #pragma unroll
