@@ -1230,28 +1230,31 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
 
     // ---- setup: hash of history / ban ids -------------------------------
+    // (history ids are fetched into registers first; LAL_GPU_MAX_HISTORY is
+    // two per thread)
+    static_assert(LAL_GPU_MAX_HISTORY <= 2 * WG && LAL_GPU_MAX_BAN_IDS <= WG, "setup registers");
+    const int h0 = (tid < nh) ? hrow[tid] : -1;
+    const int h1 = (tid + WG < nh) ? hrow[tid + WG] : -1;
+    const int bid = (tid < A.n_ban) ? A.ban_ids[tid] : -1;
     for (int s = tid; s < HSLOTS; s += WG) {
         S.hkey[s] = -1;
         S.hinfo[s] = 0;
     }
     __syncthreads();
-    for (int i = tid; i < nh; i += WG) {
-        const int t = hrow[i];
-        if (t < 0 || t >= V) continue;
+#pragma unroll
+    for (int r = 0; r < 2; ++r) {
+        const int i = tid + r * WG;
+        const int t = r ? h1 : h0;
+        if (i >= nh || t < 0 || t >= V) continue;
         int flags = 0;
         if (A.mask_recent > 0 && i >= nh - A.mask_recent) flags |= HF_MASKPRE;
         if (A.ban_last && i == nh - 1) flags |= HF_BAN;
         if (A.ban_repeat > 0 && i >= nh - A.ban_repeat) flags |= HF_BAN;
         hash_insert(S.hkey, S.hinfo, t, A.apply_pen ? 1 : 0, flags);
     }
-    for (int i = tid; i < A.n_ban; i += WG) {
-        const int t = A.ban_ids[i];
-        if (t >= 0 && t < V) hash_insert(S.hkey, S.hinfo, t, 0, HF_BAN);
-    }
+    if (bid >= 0 && bid < V) hash_insert(S.hkey, S.hinfo, bid, 0, HF_BAN);
     __syncthreads();
-    int nocc = 0;
-    for (int s = tid; s < HSLOTS; s += WG) nocc += (S.hkey[s] >= 0);
-    const bool use_hash = block_sum(S, nocc) > 0;
+    const bool use_hash = (nh > 0) || (A.n_ban > 0);
     RowCtx R;
     R.row = row;
     R.bias = A.bias;
