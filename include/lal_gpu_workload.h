@@ -50,6 +50,10 @@ int lal_gpu_synth_normal(float *d_out, size_t n, unsigned long long seed,
 int lal_gpu_synth_ids(int *d_out, size_t n, unsigned long long seed, int vocab,
                       void *stream);
 
+/* dst <- src, bytes a multiple of 16 and both 16-byte aligned: a plain
+ * streaming copy, the yardstick that hardware byte counters are scaled by. */
+int lal_gpu_copy(void *d_dst, const void *d_src, size_t bytes, void *stream);
+
 #ifdef __cplusplus
 }
 #endif

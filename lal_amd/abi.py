@@ -82,6 +82,7 @@ EXPORTS = [
     ("lal_gpu_synth_uniform", _i, [_vp, _sz, _ull, _f, _f, _vp]),
     ("lal_gpu_synth_normal", _i, [_vp, _sz, _ull, _f, _vp]),
     ("lal_gpu_synth_ids", _i, [_vp, _sz, _ull, _i, _vp]),
+    ("lal_gpu_copy", _i, [_vp, _vp, _sz, _vp]),
     ("lal_gpu_expf_check", _i, [_u, _i, _vp, _vp]),
 ]
 

@@ -1837,6 +1837,16 @@ __global__ void synth_normal_kernel(float *out, size_t n, uint64_t seed, float s
         out[i] = sigma * gauss(mix64(seed + i));
 }
 
+// Plain streaming copy (16-byte loads and stores, grid-stride): the yardstick
+// that HBM byte counters are scaled by.
+__global__ __launch_bounds__(256) void copy_f32x4_kernel(f32x4 *__restrict__ dst,
+                                                         const f32x4 *__restrict__ src, size_t n4)
+{
+    const size_t stride = (size_t)gridDim.x * blockDim.x;
+    for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += stride)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
 __global__ void synth_ids_kernel(int *out, size_t n, uint64_t seed, int V)
 {
     for (size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x; i < n; i += (size_t)gridDim.x * blockDim.x)
@@ -2259,6 +2269,20 @@ int lal_gpu_synth_ids(int *d_out, size_t n, unsigned long long seed, int vocab, 
     if (!d_out || vocab <= 0) return LAL_GPU_E_INVAL;
     hipLaunchKernelGGL(synth_ids_kernel, grid_for(n), dim3(256), 0, (hipStream_t)stream, d_out, n,
                        (uint64_t)seed, vocab);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_copy(void *d_dst, const void *d_src, size_t bytes, void *stream)
+{
+    if (!d_dst || !d_src || (bytes & 15) || ((uintptr_t)d_dst & 15) || ((uintptr_t)d_src & 15))
+        return LAL_GPU_E_INVAL;
+    const size_t n4 = bytes / 16;
+    if (n4 == 0) return LAL_GPU_OK;
+    size_t blocks = (n4 + 255) / 256;
+    if (blocks > 8192) blocks = 8192;
+    hipLaunchKernelGGL(copy_f32x4_kernel, dim3((unsigned)blocks), dim3(256), 0, (hipStream_t)stream,
+                       (f32x4 *)d_dst, (const f32x4 *)d_src, n4);
     LAL_HIP(hipGetLastError());
     return LAL_GPU_OK;
 }
