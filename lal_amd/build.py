@@ -35,13 +35,13 @@ def build_gpu_lib():
 
 
 def build_dropin_harness():
-    """C program that uses include/lal_sampling.h exactly as a LAL server does."""
-    src = os.path.join(HERE, "csrc", "dropin_harness.c")
-    if not os.path.exists(src):
-        return None
-    out = os.path.join(HERE, "dropin_harness")
-    run(["gcc", "-O2", "-Wall", "-Wextra", "-I", os.path.join(ROOT, "include"), "-o", out, src,
-         "-L", HERE, "-llal_gpu", f"-Wl,-rpath,{HERE}", "-lm"])
+    """Shared library over include/lal_sampling.h, used the way a LAL server
+    includes the reference header (tests/dropin/dropin_harness.c)."""
+    src = os.path.join(ROOT, "tests", "dropin", "dropin_harness.c")
+    out = os.path.join(ROOT, "tests", "dropin", "libdropin_harness.so")
+    run(["gcc", "-O2", "-Wall", "-Wextra", "-Wno-unused-function", "-fPIC", "-shared",
+         "-I", os.path.join(ROOT, "include"), "-o", out, src,
+         "-L", HERE, "-llal_gpu", "-Wl,-rpath,$ORIGIN/../../lal_amd", "-lm"])
     return out
 
 

@@ -1,0 +1,54 @@
+"""ctypes view of tests/dropin/libdropin_harness.so: include/lal_sampling.h
+compiled into a C translation unit, as a LAL server would include it."""
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+HARNESS = os.path.join(HERE, "dropin", "libdropin_harness.so")
+
+_fp, _ip = C.POINTER(C.c_float), C.POINTER(C.c_int)
+
+
+def _ptr(a, t):
+    return None if a is None else a.ctypes.data_as(t)
+
+
+class DropIn:
+    def __init__(self, path=HARNESS):
+        if not os.path.exists(path):
+            raise FileNotFoundError(f"{path}: run __graft_entry__.build() first")
+        L = C.CDLL(path)
+        self.L = L
+        L.dh_srand.argtypes = [C.c_uint]
+        L.dh_rand.restype = C.c_int
+        for nm in ("dh_sample_token", "dh_sample_token_filtered"):
+            f = getattr(L, nm)
+            f.restype = C.c_int
+            f.argtypes = [_fp, C.c_int, C.c_float, C.c_int, C.c_float, _ip, C.c_int]
+        L.dh_sample_token_top_p.restype = C.c_int
+        L.dh_sample_token_top_p.argtypes = [_fp, C.c_int, C.c_float, C.c_int, C.c_float]
+        L.dh_set_filter_ops.argtypes = [C.c_int, C.c_int, _ip, C.c_int]
+        L.dh_recent_push.argtypes = [_ip, _ip, C.c_int]
+        L.dh_globals.argtypes = [_ip, _ip, _fp]
+
+    def sample(self, row, T, k, pen, hist, filtered=False):
+        """row: float32 array, modified in place like the reference."""
+        h = None if hist is None else np.ascontiguousarray(hist, np.int32)
+        fn = self.L.dh_sample_token_filtered if filtered else self.L.dh_sample_token
+        return fn(_ptr(row, _fp), len(row), C.c_float(T), k, C.c_float(pen), _ptr(h, _ip),
+                  0 if h is None else len(h))
+
+    def top_p(self, row, T, k, p):
+        return self.L.dh_sample_token_top_p(_ptr(row, _fp), len(row), C.c_float(T), k, C.c_float(p))
+
+    def set_filter_ops(self, ban_last=0, ban_repeat=0, ban_ids=None):
+        ids = None if not ban_ids else np.ascontiguousarray(ban_ids, np.int32)
+        self.L.dh_set_filter_ops(ban_last, ban_repeat, _ptr(ids, _ip), 0 if ids is None else len(ids))
+
+    def srand(self, seed):
+        self.L.dh_srand(seed)
+
+    def rand(self):
+        return self.L.dh_rand()
