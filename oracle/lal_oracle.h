@@ -19,6 +19,18 @@
  *   lal_oracle_quantize_w   runtime/lal_q8_kernel.h:357-372
  *   lal_oracle_recent_push  runtime/lal_sampling.h:133-136
  *
+ * How each part is pinned (tests/):
+ *   top-k / softmax / draw / penalty / filtered variant / plugin bans:
+ *       golden vectors written by the reference's own C code
+ *       (test_oracle_golden.py) and oracle/_ref called directly;
+ *   logit-space ops (bias, allow bitmask, mask_recent): against the
+ *       reference sampler run on the op-applied row (test_oracle_pins.py);
+ *   top-p nucleus: the reference has no callable entry point; pinned by its
+ *       definition (prefix of the stable descending order that first reaches
+ *       top_p, p -> 0, p >= 1, renormalisation, draw end points) in
+ *       test_oracle_pins.py;
+ *   uniforms, Q8 quantizers, LM head, recent_push: golden vectors.
+ *
  * Unlike the reference, every routine is reentrant (per-call scratch, the
  * uniform is passed in), so the batch driver can run rows under OpenMP.
  */

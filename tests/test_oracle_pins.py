@@ -1,0 +1,166 @@
+"""Pins for the parts of the oracle that the reference's golden vectors do not
+cover directly.
+
+* Logit-space ops before selection (additive bias, allow bitmask, -inf on the
+  last n history ids) are checked against the reference's own sampler: the
+  reference penalises the row (tools/server/qwen7b_server.c:223-234), the test
+  applies the op to that row, and the reference then samples the result with
+  the penalty off.  The oracle, given the op, must return the same token.
+* The top-p nucleus (tools/server/gpt2_server.c:2908-2955; the reference has no
+  callable entry point for it) is checked through what its definition fixes:
+  the kept set is the prefix, in (probability descending, id ascending) order,
+  that first reaches top_p; p -> 0 keeps only the first maximum; p >= 1 and
+  p <= 0 leave the top-k pool untouched; the final probabilities are the
+  pool's renormalised over the kept set; u = 0 and u = 1 return the first and
+  last kept ids; the gpt2 draw returns id 0 when r == 0.
+"""
+import numpy as np
+import pytest
+
+import synth
+from oracle_lib import Oracle, Reference, make_params, VARIANT_BASIC, VARIANT_FILTERED
+
+ORC = Oracle()
+
+
+@pytest.fixture(scope="module")
+def ref():
+    try:
+        return Reference()
+    except FileNotFoundError:
+        pytest.skip("oracle/_ref not built (needs the reference tree)")
+
+
+def _allow_bits(seed, V, p):
+    rng = np.random.default_rng(seed)
+    on = rng.random(V) < p
+    words = np.zeros((V + 31) // 32, np.uint32)
+    for v in np.nonzero(on)[0]:
+        words[v >> 5] |= np.uint32(1) << np.uint32(v & 31)
+    return words, on
+
+
+@pytest.mark.parametrize("variant", [VARIANT_BASIC, VARIANT_FILTERED])
+def test_logit_ops_against_reference(ref, variant):
+    cases = 0
+    for i in range(60):
+        V = [50, 333, 1000, 4099][i % 4]
+        kind = ["gauss", "zipf", "ties", "outliers", "neginf"][i % 5]
+        row = synth.make_row(kind, 500 + i, V)
+        hist = synth.history(600 + i, 1, 24, V, with_invalid=(i % 3 == 0))[0]
+        T = [0.7, 1.3, 0.0][i % 3] if i % 7 else 0.0
+        k = [1, 7, 40, 64][i % 4]
+        pen = [1.1, 1.0, 1.3][i % 3]
+        use_bias, use_allow, nmask = i % 2 == 0, i % 3 != 1, [0, 1, 16][i % 3]
+        bias = None
+        if use_bias:
+            bias = np.zeros(V, np.float32)
+            idx = np.random.default_rng(i).choice(V, max(1, V // 10), replace=False)
+            bias[idx] = synth.normal(700 + i, 0, len(idx)) * np.float32(1.5)
+        allow, on = (None, None)
+        if use_allow:
+            allow, on = _allow_bits(800 + i, V, 0.3)
+        seed = 900 + i
+        greedy = T <= 0 or k <= 0
+
+        # the reference's own penalty (filtered sampler, greedy: penalty then argmax)
+        base = row.copy()
+        if not (variant == VARIANT_BASIC and greedy):
+            ref.sample(base, V, 0.0, k, pen, hist, seed, filtered=True)
+        y = base.copy()
+        if bias is not None:
+            y = (y + bias).astype(np.float32)
+        if allow is not None:
+            y[~on] = -np.inf
+        if nmask:
+            for t in hist[-nmask:]:
+                if 0 <= t < V:
+                    y[t] = -np.inf
+        tok_ref = ref.sample(y.copy(), V, T, k, 1.0, None, seed,
+                             filtered=(variant == VARIANT_FILTERED))
+
+        x = row.copy()
+        p = make_params(temperature=T, top_k=k, rep_penalty=pen, variant=variant, mask_recent=nmask)
+        u = ORC.uniforms(seed, 1)[0]
+        tok, *_ = ORC.sample_row(x, p, hist=hist, allow=allow, bias=bias, u=u)
+        assert tok == tok_ref, f"case {i}: oracle {tok} reference {tok_ref}"
+        assert np.array_equal(x.view(np.uint32), base.view(np.uint32)), f"case {i}: in-place row"
+        cases += 1
+    assert cases == 60
+
+
+def _pool(row, k, T):
+    """Candidates (ascending id) and their glibc-expf weights, from the oracle
+    with top-p off (the top-k path is pinned by the golden vectors)."""
+    V = len(row)
+    p = make_params(temperature=T, top_k=k, rep_penalty=1.0)
+    tok, info, ids, probs, kept = ORC.sample_row(row.copy(), p, u=0.5, cand_cap=V)
+    n = info.n_cand
+    return ids[:n].copy(), info
+
+
+def _expw(vals, T):
+    m = np.float32(-1e30)
+    for v in vals:
+        if v > m:
+            m = v
+    return np.array([ORC.expf(np.float32((np.float32(v) - m) / np.float32(T))) for v in vals],
+                    np.float32)
+
+
+@pytest.mark.parametrize("kind", ["gauss", "ties", "zipf", "outliers", "const", "descending"])
+def test_top_p_definition(kind):
+    T = 0.8
+    for j, (V, k) in enumerate(((200, 1), (500, 5), (2000, 50), (3000, 300))):
+        row = synth.make_row(kind, 40 + j, V)
+        ids, _ = _pool(row, k, T)
+        n = len(ids)
+        w = _expw(row[ids], T).astype(np.float64)
+        P = w / w.sum()
+        order = sorted(range(n), key=lambda i: (-P[i], ids[i]))
+        for top_p in (1e-6, 0.05, 0.3, 0.5, 0.9, 0.999):
+            p = make_params(temperature=T, top_k=k, top_p=top_p, rep_penalty=1.0)
+            tok, info, cids, cprobs, ckept = ORC.sample_row(row.copy(), p, u=0.5, cand_cap=V)
+            assert info.n_cand == n and np.array_equal(cids[:n], ids)
+            kept = ckept[:n].astype(bool)
+            m = int(kept.sum())
+            assert m == info.n_kept and m >= 1
+            # a prefix of the (probability desc, id asc) order
+            assert set(np.nonzero(kept)[0]) == set(order[:m]), f"{kind} V={V} k={k} p={top_p}"
+            # the first prefix whose mass reaches top_p (inclusive cutoff)
+            c = np.cumsum([P[i] for i in order])
+            assert m == n or c[m - 1] >= top_p - 1e-6
+            assert m == 1 or c[m - 2] < top_p + 1e-6
+            if top_p == 1e-6:
+                first_max = ids[int(np.argmax(row[ids]))]
+                assert m == 1 and ids[kept][0] == first_max
+            # renormalised over the kept set (fp32 sequential sums over up to
+            # 300 terms: relative error below n * 2^-24)
+            wk = w * kept
+            want = wk / wk.sum()
+            got = cprobs[:n].astype(np.float64)
+            assert np.allclose(got, want, rtol=1e-4, atol=0), f"{kind} probs"
+            assert np.all(got[~kept] == 0)
+
+
+@pytest.mark.parametrize("top_p", [0.0, 1.0, 1.5, -0.5])
+def test_top_p_off_values(top_p):
+    for kind in ("gauss", "zipf", "ties"):
+        row = synth.make_row(kind, 3, 1500)
+        for u in (0.0, 0.3, 1.0):
+            a = ORC.sample_row(row.copy(), make_params(temperature=0.9, top_k=40, top_p=top_p), u=u)[0]
+            b = ORC.sample_row(row.copy(), make_params(temperature=0.9, top_k=40), u=u)[0]
+            assert a == b
+
+
+def test_top_p_draw_endpoints():
+    for kind in ("gauss", "zipf", "ties", "outliers"):
+        row = synth.make_row(kind, 9, 3000)
+        p = make_params(temperature=0.8, top_k=100, top_p=0.7)
+        _, info, ids, _, kept = ORC.sample_row(row.copy(), p, u=0.5, cand_cap=3000)
+        kept_ids = ids[:info.n_cand][kept[:info.n_cand].astype(bool)]
+        assert ORC.sample_row(row.copy(), p, u=0.0)[0] == kept_ids[0]
+        assert ORC.sample_row(row.copy(), p, u=1.0)[0] == kept_ids[-1]
+        # gpt2 draw convention: r == 0 returns id 0 whether or not it is kept
+        pg = make_params(temperature=0.8, top_k=100, top_p=0.7, flags=0x2)
+        assert ORC.sample_row(row.copy(), pg, u=0.0)[0] == 0
