@@ -1,0 +1,124 @@
+"""GPU parity of the int8 LM head front end (runtime/lal_q8_kernel.h:375-543)
+through the C ABI: the activation quantizer (AVX2-build and scalar-build
+rounding) and the int8 LM head, against the reference's golden vectors and the
+oracle.  Bar: bit-exact (the int32 dot is exact and the scaling is the
+reference's (sx*sw)*(float)dot)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import golden_cases
+import synth
+from gpu_helpers import log
+from oracle_lib import Oracle
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from lal_amd import abi
+    d = abi.Device(0, max_batch=64, max_vocab=152064)
+    yield d
+    d.close()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return Oracle()
+
+
+def quantize(dev, x, mode):
+    from lal_amd import abi
+    B, n = x.shape
+    dx = dev.put(np.ascontiguousarray(x, np.float32))
+    dq, ds = dev.alloc(B * n), dev.alloc(4 * B)
+    abi.check(dev.lib.lal_gpu_quantize_x(dev.ctx, dx.ptr, B, n, mode, dq.ptr, ds.ptr, dev.stream),
+              "quantize_x")
+    dev.sync()
+    q, s = dq.download((B, n), np.int8), ds.download(B, np.float32)
+    for b in (dx, dq, ds):
+        b.close()
+    return s, q
+
+
+def lm_head(dev, xq, sx, W, sw, ld=None, offset=0):
+    from lal_amd import abi
+    B, n = xq.shape
+    V = W.shape[0]
+    ld = V if ld is None else ld
+    # `offset` shifts the weight rows off 16-byte alignment to cover the byte-load kernel
+    dW = dev.alloc(W.size + 64)
+    buf = np.zeros(W.size + 64, np.int8)
+    buf[offset:offset + W.size] = W.reshape(-1)
+    abi.check(dev.lib.lal_gpu_memcpy_h2d(dW.ptr, buf.ctypes.data, buf.nbytes, dev.stream), "h2d")
+    dq, ds, dsw = dev.put(np.ascontiguousarray(xq)), dev.put(np.asarray(sx, np.float32)), dev.put(sw)
+    dl = dev.alloc(4 * B * ld)
+    abi.check(dev.lib.lal_gpu_lm_head_q8(dev.ctx, dq.ptr, ds.ptr, B, n, C.c_void_p(dW.ptr + offset),
+                                         dsw.ptr, V, dl.ptr, ld, dev.stream), "lm_head")
+    dev.sync()
+    out = dl.download((B, ld), np.float32)[:, :V].copy()
+    for b in (dW, dq, ds, dsw, dl):
+        b.close()
+    return out
+
+
+def test_quantize_x_golden(dev):
+    for rec in golden_cases.load()["q8"]["quantize_x"]:
+        x = (synth.normal(rec["seed"], 0, rec["n"]) * np.float32(rec["scale"])).astype(np.float32)
+        for mode, sfx in ((0, "avx2"), (1, "scalar")):
+            s, q = quantize(dev, x[None, :], mode)
+            log(f"quantize_x n={rec['n']} {sfx}")
+            assert s[0].view(np.uint32) == rec[sfx]["scale_bits"]
+            assert q[0].tobytes().hex() == rec[sfx]["xq"]
+
+
+def test_lm_head_golden(dev):
+    for rec in golden_cases.load()["q8"]["lm_head"]:
+        V, n, seed = rec["V"], rec["n"], rec["seed"]
+        W = synth.ints(seed, 1, V * n, -127, 128).astype(np.int8).reshape(V, n)
+        sw = (synth.uniform(seed, 2, V) * np.float32(0.019) + np.float32(0.001)).astype(np.float32)
+        xq = np.frombuffer(bytes.fromhex(rec["xq"]), np.int8).copy()[None, :]
+        sx = np.array([golden_cases.f32(rec["sx_bits"])], np.float32)
+        for offset in (0, 3):
+            log(f"lm_head golden V={V} n={n} offset={offset}")
+            out = lm_head(dev, xq, sx, W, sw, offset=offset)
+            assert list(out[0].view(np.uint32)) == rec["lm_head_int8_range_scalar"]
+
+
+@pytest.mark.parametrize("B", [1, 3, 16, 64])
+def test_lm_head_qwen7b_shape(dev, orc, B):
+    """Hidden [B, 3584] ~ N(0,1) quantized per row (AVX2 build), W [152064, 3584]
+    int8 in [-127, 127], sw ~ U(0.001, 0.02); every logit of a 4096-row sample of
+    the vocabulary checked against the oracle, plus the quantizer in full."""
+    from lal_amd import abi
+    V, n = 152064, 3584
+    x = synth.normal(50 + B, 0, B * n).reshape(B, n).astype(np.float32)
+    s, q = quantize(dev, x, 0)
+    for b in range(B):
+        so, qo = orc.quantize_x(x[b].copy(), 0)
+        assert s[b].view(np.uint32) == so.view(np.uint32) and np.array_equal(q[b], qo)
+    dW = dev.alloc(V * n)
+    abi.check(dev.lib.lal_gpu_synth_int8(dW.ptr, V * n, 77, -127, 127, dev.stream), "synth W")
+    dsw = dev.alloc(4 * V)
+    abi.check(dev.lib.lal_gpu_synth_uniform(dsw.ptr, V, 78, C.c_float(0.001), C.c_float(0.02),
+                                            dev.stream), "synth sw")
+    dq, ds = dev.put(q), dev.put(s)
+    dl = dev.alloc(4 * B * V)
+    abi.check(dev.lib.lal_gpu_lm_head_q8(dev.ctx, dq.ptr, ds.ptr, B, n, dW.ptr, dsw.ptr, V, dl.ptr,
+                                         V, dev.stream), "lm_head")
+    dev.sync()
+    out = dl.download((B, V), np.float32)
+    rows = np.sort(np.random.default_rng(B).choice(V, 4096, replace=False))
+    sw = dsw.download(V, np.float32)
+    Wall = dW.download((V, n), np.int8)
+    Ws = np.ascontiguousarray(Wall[rows])
+    del Wall
+    for b in range(B):
+        want = orc.lm_head(q[b].copy(), s[b], Ws, np.ascontiguousarray(sw[rows]))
+        got = out[b, rows]
+        assert np.array_equal(got.view(np.uint32), want.view(np.uint32)), f"row {b}"
+    log(f"lm_head B={B}: {len(rows)} vocab rows x {B} bit-exact")
+    for bb in (dW, dsw, dq, ds, dl):
+        bb.close()
