@@ -111,8 +111,13 @@ typedef struct lal_gpu_sample_io {
                                          penalty for each history position */
 } lal_gpu_sample_io;
 
-/* Context: owns per-device scratch sized for max_batch x max_vocab.
- * One context per host thread / stream. */
+/* Context: owns per-device scratch for up to max_batch rows (candidate lists
+ * exchanged between the workgroups of one row, 64 KiB per row, and one counter
+ * per row).  One context per host thread / stream: calls that overlap on one
+ * context race.  Rows may be split into slices, one workgroup each, when the
+ * batch is too small to fill the GPU; the environment variable
+ * LAL_GPU_SLICES (1..64) overrides that choice (tuning only; results do not
+ * depend on it). */
 int  lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab);
 void lal_gpu_destroy(lal_gpu_ctx *ctx);
 

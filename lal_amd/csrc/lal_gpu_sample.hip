@@ -56,6 +56,8 @@ constexpr int RS_CHUNK = NWAVE * 256;         // rescan chunk (lives in the hist
 constexpr int CAPW_SMALL = 512;
 constexpr int CAPW_LARGE = 2048;
 constexpr int K_SMALL_MAX = 128;
+constexpr int MAX_SLICES = 64;                 // slices per row
+constexpr int FLAT_MAX = NWAVE * CAPW_LARGE;   // slice-list entries per row
 // row sample for the threshold estimate: 64 float4 (1 KB) every SBLK float4
 constexpr int SBLK = 2048;          // 32 KB stride -> 1/32 of the row
 constexpr int SR = 5;               // float4 per thread: up to 20 sampled blocks (V <= 163840 fully sampled)
@@ -81,7 +83,7 @@ __constant__ uint64_t kExp2Tab[32] = {
     0x3feee89f995ad3adull, 0x3feeff76f2fb5e47ull, 0x3fef199bdd85529cull, 0x3fef3720dcef9069ull,
     0x3fef5818dcfba487ull, 0x3fef7c97337b9b5full, 0x3fefa4afa2a490daull, 0x3fefd0765b6e4540ull};
 
-__device__ __forceinline__ float glibc_expf(float x)
+__device__ __forceinline__ float glibc_expf(float x, const uint64_t *tab)
 {
     const uint32_t ux = __float_as_uint(x);
     const uint32_t abstop = (ux >> 20) & 0x7ff;
@@ -101,7 +103,7 @@ __device__ __forceinline__ float glibc_expf(float x)
     const uint64_t ki = (uint64_t)__double_as_longlong(kd);
     kd -= Shift;
     const double r = __fma_rn(InvLn2N, xd, -kd);
-    uint64_t t = kExp2Tab[ki & 31];
+    uint64_t t = tab[ki & 31];
     t += ki << 47;
     const double s = __longlong_as_double((long long)t);
     const double z = __fma_rn(C0, r, C1);
@@ -180,6 +182,35 @@ __device__ __forceinline__ float readlane_f(float v, int l)
     return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), l));
 }
 
+// Device-coherent (agent-scope) plain accesses, for data exchanged between
+// workgroups of one launch.
+template <class T>
+__device__ __forceinline__ void dev_store(T *p, T v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T dev_load(const T *p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Wave issue priority (0..3).  Streaming waves lower theirs as they progress,
+// so a wave that is behind (e.g. the youngest workgroup on a CU, which the
+// age-ordered arbiter serves last) is served first; latency-bound phases run
+// at the top level.
+__device__ __forceinline__ void set_wave_prio(int level)
+{
+    switch (level) {
+    case 0: __builtin_amdgcn_s_setprio(0); break;
+    case 1: __builtin_amdgcn_s_setprio(1); break;
+    case 2: __builtin_amdgcn_s_setprio(2); break;
+    default: __builtin_amdgcn_s_setprio(3); break;
+    }
+}
+
+// Wait until this thread's outstanding memory operations have completed.
+__device__ __forceinline__ void wait_stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 template <int CAPW>
 struct Smem {
     float cval[NWAVE * CAPW];  // per-wave candidate buffers: exact processed logits
@@ -204,6 +235,7 @@ struct Smem {
     int redi2[NWAVE];
     int sel_digit;
     int sel_rem;
+    uint64_t exptab[32];  // glibc's 2^(i/32) table (LDS copy of kExp2Tab)
 };
 
 struct KArgs {
@@ -237,6 +269,16 @@ struct KArgs {
     int greedy;     // greedy path: k = 1, first index among the maxima
     int apply_pen;  // penalty applied for this variant / greedy state
     int any_bans;
+    // slicing: each row is split into nslice contiguous slices, one workgroup
+    // each; a slice publishes its candidates (at most lcap) and the last slice
+    // to arrive finishes the row
+    int batch;
+    int nslice;
+    int lcap;
+    float *lst_val;     // [batch][nslice][lcap] candidate values
+    int *lst_idx;       // [batch][nslice][lcap] candidate ids
+    int4 *lst_meta;     // [batch][nslice] (count, threshold bits, strict, -)
+    unsigned *arrive;   // [batch] slices finished; reset by the finisher
 };
 
 // block reductions (barriers inside; callers keep control flow uniform)
@@ -465,7 +507,10 @@ __device__ __forceinline__ float exact_value(const RowCtx &R, int e, float yhat)
         const int s = hash_find(R.hkey, e);
         if (s >= 0) {
             const int info = R.hinfo[s];
-            float y = penalise(R.row[e], info & HCOUNT_MASK, R.pen);
+            // without a bias the upper bound is the raw logit (or -inf when
+            // the allow bit is clear, which the mask below keeps)
+            const float raw = R.has_bias ? R.row[e] : yhat;
+            float y = penalise(raw, info & HCOUNT_MASK, R.pen);
             if (R.has_bias) y = y + R.bias[e];
             if (R.has_allow && !allow_bit(R.abits, e)) y = -INFINITY;
             if (info & HF_MASKPRE) y = -INFINITY;
@@ -503,6 +548,18 @@ __device__ __forceinline__ uint32_t wave_merge_top_desc(uint32_t a, uint32_t b)
         key = ((lane & stride) == 0) ? max(key, other) : min(key, other);
     }
     return key;
+}
+
+// k-th largest of the 64 lane keys (1 <= k <= 64), bit by bit: the largest K
+// with at least k keys >= K.  Ballot counts only; wave-synchronous.
+__device__ __forceinline__ uint32_t wave_kth_lane_key(uint32_t key, int k)
+{
+    uint32_t K = 0u;
+    for (int bit = 31; bit >= 0; --bit) {
+        const uint32_t cand = K | (1u << bit);
+        if (__popcll(__ballot(key >= cand)) >= k) K = cand;
+    }
+    return K;
 }
 
 // ---------------------------------------------------------------------------
@@ -699,7 +756,22 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
     float tk = st.tau;
     bool strict = st.strict;
     if (cnt + offered > CAPW) {
-        tk = keyf(wave_kth_key<NV>(hist, bv, cnt, y, m, k));
+        if (k <= 64) {
+            // the k-th largest of the lanes' maxima: k distinct values of the
+            // set, so no larger than its k-th largest (a valid, cheap bound;
+            // every lane holds at least CAPW/64 values here)
+            uint32_t mk = 0u;
+#pragma unroll
+            for (int i = 0; i < NV; ++i)
+                if ((m >> i) & 1u) mk = max(mk, fkey(y[i]));
+            for (int j = lane_id(); j < cnt; j += 64) {
+                const float v = bv[j];
+                if (v == v) mk = max(mk, fkey(v));
+            }
+            tk = keyf(wave_kth_lane_key(mk, k));
+        } else {
+            tk = keyf(wave_kth_key<NV>(hist, bv, cnt, y, m, k));
+        }
         int nge = 0;
         for (int j = lane_id(); j < cnt; j += 64) nge += (bv[j] >= tk);
 #pragma unroll
@@ -840,6 +912,24 @@ __device__ __forceinline__ bool is_banned(const SM &S, int e)
     return s >= 0 && (S.hinfo[s] & HF_BAN);
 }
 
+// The top-p nucleus of a rescanned row (gpt2_server.c:2908-2955): in the
+// order (probability desc, id asc) the kept tokens are a prefix, so the set is
+// {p > plim} plus {p == plim and id <= idlim}, p = expf((y - amax)/T) * inv.
+struct Nucleus {
+    bool on;
+    float amax, inv, plim;
+    int idlim;
+};
+
+template <class SM>
+__device__ __forceinline__ bool in_nucleus(const KArgs &A, const SM &S, const Nucleus &N, float y,
+                                           int e)
+{
+    if (!N.on) return true;
+    const float p = glibc_expf((y - N.amax) / A.T, S.exptab) * N.inv;
+    return p > N.plim || (p == N.plim && e <= N.idlim);
+}
+
 struct RescanStats {
     int n_cand, n_kept;
     float max_kept;     // max over the set, plain max (no -1e30 floor)
@@ -850,7 +940,7 @@ struct RescanStats {
 template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
 __device__ __forceinline__ RescanStats rescan_stats(const KArgs &A, SM &S, const float *row,
                                                     const uint32_t *abits, bool use_hash, float T,
-                                                    bool use_ban)
+                                                    bool use_ban, const Nucleus &N)
 {
     int nc = 0, nk = 0, first = INT_MAX;
     float mk = -INFINITY;
@@ -858,6 +948,7 @@ __device__ __forceinline__ RescanStats rescan_stats(const KArgs &A, SM &S, const
         const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
         if (!(yv >= T)) continue;
         nc++;
+        if (!in_nucleus(A, S, N, yv, e)) continue;
         if (use_ban && is_banned(S, e)) continue;
         nk++;
         mk = fmaxf(mk, yv);
@@ -872,6 +963,7 @@ __device__ __forceinline__ RescanStats rescan_stats(const KArgs &A, SM &S, const
     for (int e = threadIdx.x; e < A.V; e += WG) {
         const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
         if (!(yv >= T) || !(yv == st.max_kept)) continue;
+        if (!in_nucleus(A, S, N, yv, e)) continue;
         if (use_ban && is_banned(S, e)) continue;
         fm = min(fm, e);
     }
@@ -885,8 +977,8 @@ __device__ __forceinline__ RescanStats rescan_stats(const KArgs &A, SM &S, const
 template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
 __device__ __forceinline__ float rescan_sequential(const KArgs &A, SM &S, const float *row,
                                                    const uint32_t *abits, bool use_hash, float T,
-                                                   bool use_ban, float mx, bool draw, float r,
-                                                   int *token)
+                                                   bool use_ban, const Nucleus &N, float mx,
+                                                   bool draw, float r, int *token)
 {
     float *ep = S.u.ep + HSLOTS;  // histogram area; hval stays intact
     float acc = 0.0f;
@@ -902,8 +994,8 @@ __device__ __forceinline__ float rescan_sequential(const KArgs &A, SM &S, const 
             if (i < n) {
                 const int e = c0 + i;
                 const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
-                kept[q] = (yv >= T) && !(use_ban && is_banned(S, e));
-                ep[i] = kept[q] ? glibc_expf((yv - mx) / A.T) : -1.0f;
+                kept[q] = (yv >= T) && in_nucleus(A, S, N, yv, e) && !(use_ban && is_banned(S, e));
+                ep[i] = kept[q] ? glibc_expf((yv - mx) / A.T, S.exptab) : -1.0f;
             }
         }
         acc = block_seq_prefix(S, ep, n, acc);
@@ -930,8 +1022,8 @@ __device__ __forceinline__ float rescan_sequential(const KArgs &A, SM &S, const 
 template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
 __device__ __forceinline__ void rescan_write_cands(const KArgs &A, SM &S, const float *row,
                                                    const uint32_t *abits, bool use_hash, float T,
-                                                   bool use_ban, float mx, float sum, bool greedy,
-                                                   int greedy_token, int b)
+                                                   bool use_ban, const Nucleus &N, float mx, float sum,
+                                                   bool greedy, int greedy_token, int b)
 {
     constexpr int PT = RS_CHUNK / WG;
     int written = 0;
@@ -961,19 +1053,148 @@ __device__ __forceinline__ void rescan_write_cands(const KArgs &A, SM &S, const 
             if (e_of[q] < 0) continue;
             if (pos < A.cand_ld) {
                 const int e = e_of[q];
-                const bool kept = greedy ? (e == greedy_token) : !(use_ban && is_banned(S, e));
+                const bool kept = greedy ? (e == greedy_token)
+                                         : in_nucleus(A, S, N, y_of[q], e) && !(use_ban && is_banned(S, e));
                 const size_t o = (size_t)b * A.cand_ld + pos;
                 if (A.cand_ids) A.cand_ids[o] = e;
                 if (A.cand_kept) A.cand_kept[o] = kept ? 1 : 0;
                 if (A.cand_probs)
                     A.cand_probs[o] = greedy ? (kept ? 1.0f : 0.0f)
-                                             : (kept ? glibc_expf((y_of[q] - mx) / A.T) / sum : 0.0f);
+                                             : (kept ? glibc_expf((y_of[q] - mx) / A.T, S.exptab) / sum : 0.0f);
             }
             pos++;
         }
         written += tot;
         __syncthreads();
     }
+}
+
+// The nucleus of a pool too large for the buffers.  All pool values are
+// >= T and fewer than k exceed it, so the entries with p above p_T =
+// p(T) (set A, fewer than k) are gathered and ranked in LDS; the rest share
+// p == p_T and follow A in id order.  The cumulative mass is added
+// sequentially in that order until it reaches top_p.
+template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
+__device__ __forceinline__ Nucleus rescan_nucleus(const KArgs &A, SM &S, const float *row,
+                                                  const uint32_t *abits, bool use_hash, float T,
+                                                  int n_cand, float pool_max)
+{
+    Nucleus N;
+    N.on = false;
+    N.amax = (pool_max > -1e30f) ? pool_max : -1e30f;
+    const float se = rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false, N,
+                                                            N.amax, false, 0.0f, nullptr);
+    N.inv = 1.0f / (se + 1e-12f);
+    const float pT = glibc_expf((T - N.amax) / A.T, S.exptab) * N.inv;
+    // gather A
+    float *ap = S.cval;
+    int *aid = S.cidx;
+    float *sp = S.cval + LAL_GPU_MAX_K;
+    int *sid = S.cidx + LAL_GPU_MAX_K;
+    __syncthreads();
+    if (threadIdx.x == 0) S.sel_rem = 0;
+    __syncthreads();
+    for (int e = threadIdx.x; e < A.V; e += WG) {
+        const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
+        if (!(yv > T)) continue;
+        const float p = glibc_expf((yv - N.amax) / A.T, S.exptab) * N.inv;
+        if (!(p > pT)) continue;
+        const int slot = atomicAdd(&S.sel_rem, 1);
+        if (slot < LAL_GPU_MAX_K) {
+            ap[slot] = p;
+            aid[slot] = e;
+        }
+    }
+    __syncthreads();
+    const int na = min(S.sel_rem, LAL_GPU_MAX_K);
+    // rank A by (p desc, id asc)
+    for (int i = threadIdx.x; i < na; i += WG) {
+        const float pi = ap[i];
+        const int ii = aid[i];
+        int rank = 0;
+        for (int j = 0; j < na; ++j) {
+            const float pj = ap[j];
+            rank += (pj > pi) || (pj == pi && aid[j] < ii);
+        }
+        sp[rank] = pi;
+        sid[rank] = ii;
+    }
+    __syncthreads();
+    // cumulative mass in sorted order (one thread: the reference's order)
+    if (threadIdx.x == 0) {
+        float cum = 0.0f;
+        int cut = -1;
+        for (int i = 0; i < na; ++i) {
+            cum = cum + sp[i];
+            if (cum >= A.top_p) {
+                cut = i;
+                break;
+            }
+        }
+        int jg = 0;  // tokens of the tie group kept (0: cut inside A; n_g: all)
+        const int ng = n_cand - na;
+        if (cut < 0) {
+            jg = ng;
+            for (int j = 1; j <= ng; ++j) {
+                cum = cum + pT;
+                if (cum >= A.top_p) {
+                    jg = j;
+                    break;
+                }
+            }
+        }
+        S.redf[0] = (cut >= 0) ? sp[cut] : pT;
+        S.redi[0] = (cut >= 0) ? sid[cut] : -1;
+        S.redi2[0] = (cut >= 0) ? 0 : jg;
+    }
+    __syncthreads();
+    N.on = true;
+    N.plim = S.redf[0];
+    N.idlim = S.redi[0];
+    const int jg = S.redi2[0];
+    __syncthreads();
+    if (N.idlim < 0) {
+        // the cut falls in the tie group: the id of its jg-th member (id order)
+        constexpr int PT = RS_CHUNK / WG;
+        int seen = 0, found = A.V;
+        for (int c0 = 0; c0 < A.V && jg > 0; c0 += RS_CHUNK) {
+            const int n = min(RS_CHUNK, A.V - c0);
+            int mine = 0;
+            bool g[PT];
+#pragma unroll
+            for (int q = 0; q < PT; ++q) {
+                const int i = (int)threadIdx.x * PT + q;  // contiguous ids per thread
+                g[q] = false;
+                if (i < n) {
+                    const int e = c0 + i;
+                    const float yv = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, e);
+                    if (yv >= T) {
+                        const float p = glibc_expf((yv - N.amax) / A.T, S.exptab) * N.inv;
+                        g[q] = (p == pT);
+                    }
+                    mine += g[q];
+                }
+            }
+            int tot;
+            int pos = seen + block_excl_scan(mine, tot, S.wsum[(c0 / RS_CHUNK) & 1]);
+            int hit = INT_MAX;
+#pragma unroll
+            for (int q = 0; q < PT; ++q) {
+                if (!g[q]) continue;
+                pos++;
+                if (pos == jg) hit = c0 + (int)threadIdx.x * PT + q;
+            }
+            hit = block_min(S, hit);
+            seen += tot;
+            if (hit != INT_MAX) {
+                found = hit;
+                break;
+            }
+        }
+        N.idlim = found;
+        N.plim = pT;
+    }
+    return N;
 }
 
 // ---------------------------------------------------------------------------
@@ -985,6 +1206,58 @@ struct RowResult {
     float sum;
 };
 
+// Sequential fp32 helpers over one wave's 64 values staged in LDS (buf,
+// 64 floats): every lane runs the same addition chain in index order, which is
+// the reference's scalar loop order.  Values that are not in the set must be
+// +0.0 (adding +0.0 to a sum of non-negative terms leaves it unchanged).
+struct Staged64 {
+    f32x4 q[16];
+};
+
+__device__ __forceinline__ Staged64 load_staged(const float *buf)
+{
+    Staged64 s;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) s.q[i] = reinterpret_cast<const f32x4 *>(buf)[i];
+    return s;
+}
+
+// Sum of the 64 staged values in index order (entries past the set are +0.0).
+__device__ __forceinline__ float seq_total(const float *buf)
+{
+    const Staged64 s = load_staged(buf);
+    float acc = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        acc = acc + s.q[i][0];
+        acc = acc + s.q[i][1];
+        acc = acc + s.q[i][2];
+        acc = acc + s.q[i][3];
+    }
+    return acc;
+}
+
+// First index i < n whose inclusive sequential prefix reaches `target`
+// (prefix >= target); n if none.  The prefix never decreases (non-negative
+// terms), so the index is the number of prefixes that do not reach target.
+__device__ __forceinline__ int seq_first_reach(const float *buf, int n, float target)
+{
+    const Staged64 s = load_staged(buf);
+    float acc = 0.0f;
+    int below = 0;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            acc = acc + s.q[i][c];
+            below += !(acc >= target) ? 1 : 0;  // a nan target is never reached
+        }
+    }
+    return min(below, n);
+}
+
+// Pool of at most 64 candidates, one per lane in ascending id order (S.cval /
+// S.cidx [0, nc)), handled by one wave.
 template <class SM>
 __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc, float u, int b)
 {
@@ -993,30 +1266,38 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
     const float y = valid ? S.cval[lane] : -INFINITY;
     const int id = valid ? S.cidx[lane] : -1;
     const bool ban = valid && A.any_bans && is_banned(S, id);
+    float *buf = S.u.ep;          // 64 staged values
+    float *buf2 = S.u.ep + 64;    // sorted probabilities
     bool nuc = valid;
-    if (A.top_p > 0.0f && A.top_p < 1.0f) {
+    float amax = -1e30f, e1 = 0.0f;
+    const bool top_p_on = A.top_p > 0.0f && A.top_p < 1.0f;
+    if (top_p_on) {
         // gpt2_server.c:2908-2955: probabilities over the pool, stable sort
         // by descending probability, inclusive cumulative cutoff
-        float amax = wave_max(valid ? y : -INFINITY);
+        amax = wave_max(valid ? y : -INFINITY);
         if (!(amax > -1e30f)) amax = -1e30f;
-        const float e1 = valid ? glibc_expf((y - amax) / A.T) : -1.0f;
-        float se;
-        (void)wave_seq_prefix(e1, nc, &se);
-        const float inv = 1.0f / (se + 1e-12f);
-        const float p = valid ? e1 * inv : 0.0f;
-        int rank = 0;
-        for (int j = 0; j < nc; ++j) {
-            const float pj = readlane_f(p, j);
-            rank += (pj > p) || (pj == p && j < lane);
-        }
-        float *ep = S.u.ep;
-        if (valid) ep[rank] = p;
+        e1 = valid ? glibc_expf((y - amax) / A.T, S.exptab) : 0.0f;
+        buf[lane] = e1;
         wave_sync();
-        const float ps = valid ? ep[lane] : -1.0f;
-        float tot;
-        const float cum = wave_seq_prefix(ps, nc, &tot);
-        const unsigned long long reach = __ballot(valid && cum >= A.top_p);
-        const int cut = reach ? (int)__builtin_ctzll(reach) : nc - 1;
+        const float se = seq_total(buf);
+        const float inv = 1.0f / (se + 1e-12f);
+        const float p = valid ? e1 * inv : -1.0f;
+        // rank in (probability desc, id asc) order: 64-bit keys, larger first
+        const uint64_t key = valid ? (((uint64_t)fkey(p) << 32) | (uint32_t)(63 - lane)) : 0ull;
+        uint64_t *kb = reinterpret_cast<uint64_t *>(S.u.ep + 128);
+        kb[lane] = key;
+        wave_sync();
+        int rank = 0;
+        for (int j = 0; j < nc; j += 2) {
+            const uint64_t k0 = kb[j], k1 = kb[j + 1];
+            rank += (k0 > key);
+            rank += (j + 1 < nc) && (k1 > key);
+        }
+        buf2[lane] = 0.0f;
+        wave_sync();
+        if (valid) buf2[rank] = p;
+        wave_sync();
+        const int cut = min(seq_first_reach(buf2, nc, A.top_p), nc - 1);
         nuc = valid && rank <= cut;
         wave_sync();
     }
@@ -1025,9 +1306,11 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
     const int n_kept = __popcll(__ballot(kept));
     const float kmax = wave_max(kept ? y : -INFINITY);
     const float mx = (kmax > -1e30f) ? kmax : -1e30f;
-    const float e2 = kept ? glibc_expf((y - mx) / A.T) : -1.0f;
-    float sum;
-    const float pre = wave_seq_prefix(e2, nc, &sum);
+    // same inputs as e1 when the maximum is kept: reuse it
+    const float e2 = !kept ? 0.0f : (top_p_on && mx == amax) ? e1 : glibc_expf((y - mx) / A.T, S.exptab);
+    buf[lane] = e2;
+    wave_sync();
+    const float sum = seq_total(buf);
     RowResult res;
     res.n_kept = n_kept;
     res.sum = sum;
@@ -1039,8 +1322,17 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
         if ((A.flags & LAL_GPU_F_DRAW_GPT2) && r == 0.0f) {
             res.token = 0;
         } else {
-            const unsigned long long hm = __ballot(kept && r <= pre);
-            res.token = hm ? readlane_i(id, (int)__builtin_ctzll(hm)) : A.V - 1;
+            // first kept candidate (id order) whose prefix reaches r.  A
+            // non-kept entry carries its predecessor's prefix, so for r > 0 the
+            // first index found is kept; for r <= 0 it is the first kept one.
+            int f;
+            if (r <= 0.0f) {
+                const unsigned long long hk = __ballot(kept);
+                f = hk ? (int)__builtin_ctzll(hk) : nc;
+            } else {
+                f = seq_first_reach(buf, nc, r);
+            }
+            res.token = (f < nc) ? readlane_i(id, f) : A.V - 1;
         }
     }
     if (valid && lane < A.cand_ld) {
@@ -1049,6 +1341,7 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
         if (A.cand_kept) A.cand_kept[o] = kept ? 1 : 0;
         if (A.cand_probs) A.cand_probs[o] = kept ? e2 / sum : 0.0f;
     }
+    wave_sync();
     return res;
 }
 
@@ -1078,7 +1371,7 @@ __device__ __forceinline__ RowResult block_epilogue(const KArgs &A, SM &S, int n
 #pragma unroll
         for (int r = 0; r < PER; ++r) {
             const int j = tid + r * WG;
-            e1[r] = (j < nc) ? glibc_expf((yv[r] - amax) / A.T) : 0.0f;
+            e1[r] = (j < nc) ? glibc_expf((yv[r] - amax) / A.T, S.exptab) : 0.0f;
             if (j < nc) ep[j] = e1[r];
         }
         const float se = block_seq_prefix(S, ep, nc, 0.0f);
@@ -1144,7 +1437,7 @@ __device__ __forceinline__ RowResult block_epilogue(const KArgs &A, SM &S, int n
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
         const int j = tid + r * WG;
-        e2[r] = kept[r] ? glibc_expf((yv[r] - mx) / A.T) : 0.0f;
+        e2[r] = kept[r] ? glibc_expf((yv[r] - mx) / A.T, S.exptab) : 0.0f;
         if (j < nc) ep[j] = kept[r] ? e2[r] : -1.0f;
     }
     res.sum = block_seq_prefix(S, ep, nc, 0.0f);
@@ -1191,7 +1484,20 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 {
     __shared__ Smem<CAPW> S;
     constexpr int PER = NWAVE * CAPW / WG;  // union entries per thread
-    const int b = blockIdx.x;
+    // work unit: slice `sl` of row `b`.  Rows go in groups of 8 with the
+    // slices of one row 8 workgroups apart, so that (with workgroups dealt
+    // round-robin to the 8 XCDs) every slice of a row runs on the same XCD
+    // and its list exchange stays in that XCD's L2.
+    const int nsl = A.nslice;
+    int b, sl;
+    {
+        const int per_grp = 8 * nsl;
+        const int gi = blockIdx.x / per_grp;
+        const int r = blockIdx.x - gi * per_grp;
+        sl = r >> 3;
+        b = gi * 8 + (r & 7);
+    }
+    if (b >= A.batch) return;
     const int tid = threadIdx.x;
     const int w = wave_id(), lane = lane_id();
     const int V = A.V;
@@ -1203,16 +1509,35 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         nh = A.hist_len ? A.hist_len[b] : A.hist_ld;
         nh = max(0, min(nh, A.hist_ld));
     }
+    // history / ban ids first: the setup waits for these loads only
+    // (LAL_GPU_MAX_HISTORY is two per thread)
+    static_assert(LAL_GPU_MAX_HISTORY <= 2 * WG && LAL_GPU_MAX_BAN_IDS <= WG, "setup registers");
+    const int h0 = (tid < nh) ? hrow[tid] : -1;
+    const int h1 = (tid + WG < nh) ? hrow[tid + WG] : -1;
+    const int bid = (tid < A.n_ban) ? A.ban_ids[tid] : -1;
+    const float uu = (A.uniforms && !A.greedy) ? A.uniforms[b] : 0.0f;
+
     const RowGeo g = row_geo(row, V);
     const int k = A.greedy ? 1 : min(max(A.k, 1), V);
 
-    // this wave's contiguous share of the aligned body
-    const int qb = (int)(((long long)g.nb4 * w) / NWAVE);
-    const int qe = (int)(((long long)g.nb4 * (w + 1)) / NWAVE);
+    // this slice's quads of the aligned body, and this wave's contiguous share
+    const int sb = (int)(((long long)g.nb4 * sl) / nsl);
+    const int se = (int)(((long long)g.nb4 * (sl + 1)) / nsl);
+    const int qb = sb + (int)(((long long)(se - sb) * w) / NWAVE);
+    const int qe = sb + (int)(((long long)(se - sb) * (w + 1)) / NWAVE);
+    const bool has_extras = (sl == 0) && (g.head + g.ntail > 0);
+    const int vlen = 4 * (se - sb) + (has_extras ? g.head + g.ntail : 0);
     const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
 
-    // the first two iterations' loads and the row sample go out before the
+    // the slice sample and the first two iterations' loads go out before the
     // hash setup
+    f32x4 smp[SR];
+#pragma unroll
+    for (int r = 0; r < SR; ++r) {
+        const int sidx = tid + WG * r;
+        const int q = sb + (sidx >> 6) * SBLK + (sidx & 63);
+        smp[r] = (q < se) ? row4[q] : f32x4{NAN, NAN, NAN, NAN};
+    }
     f32x4 cur[U4], nx1[U4];
 #pragma unroll
     for (int u = 0; u < U4; ++u) {
@@ -1221,25 +1546,13 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const int q1 = qb + WITER + u * 64 + lane;
         nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
     }
-    f32x4 smp[SR];
-#pragma unroll
-    for (int r = 0; r < SR; ++r) {
-        const int sidx = tid + WG * r;
-        const int q = (sidx >> 6) * SBLK + (sidx & 63);
-        smp[r] = (q < g.nb4) ? row4[q] : f32x4{NAN, NAN, NAN, NAN};
-    }
 
     // ---- setup: hash of history / ban ids -------------------------------
-    // (history ids are fetched into registers first; LAL_GPU_MAX_HISTORY is
-    // two per thread)
-    static_assert(LAL_GPU_MAX_HISTORY <= 2 * WG && LAL_GPU_MAX_BAN_IDS <= WG, "setup registers");
-    const int h0 = (tid < nh) ? hrow[tid] : -1;
-    const int h1 = (tid + WG < nh) ? hrow[tid + WG] : -1;
-    const int bid = (tid < A.n_ban) ? A.ban_ids[tid] : -1;
     for (int s = tid; s < HSLOTS; s += WG) {
         S.hkey[s] = -1;
         S.hinfo[s] = 0;
     }
+    if (tid < 32) S.exptab[tid] = kExp2Tab[tid];
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -1280,8 +1593,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 #pragma unroll
         for (int r = 0; r < SR; ++r) {
             const int sidx = tid + WG * r;
-            const int q = (sidx >> 6) * SBLK + (sidx & 63);
-            if (q < g.nb4) {
+            const int q = sb + (sidx >> 6) * SBLK + (sidx & 63);
+            if (q < se) {
 #pragma unroll
                 for (int c = 0; c < 4; ++c) {
                     const float v = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, g.head + 4 * q + c,
@@ -1292,7 +1605,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             }
         }
         const int nsmp = block_sum(S, nvalid);
-        const float lam = (float)k * (float)nsmp / (float)V;
+        const float lam = (float)k * (float)nsmp / (float)max(vlen, 1);
         const int ks = (int)ceilf(lam + 6.0f * sqrtf(lam) + 6.0f);
         if (!A.greedy && nsmp > 0 && ks <= 64) {
             unsigned *tmp = S.u.h.whist[0];  // 4 x 64 keys
@@ -1336,15 +1649,24 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         st.cnt = 0;
 
     // ---- stream: each wave owns its share, no workgroup barrier ----------
-    if (w == 0 && g.head + g.ntail > 0) {
-        // head / tail elements outside the aligned body
+    if (w == 0 && has_extras) {
+        // head / tail elements outside the aligned body (slice 0)
         const int e = extra_elem(g, lane);
         float x[4] = {NAN, NAN, NAN, NAN};
         const int eb[1] = {e};
         if (e >= 0) x[0] = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
         wave_offer<1, CAPW>(bv, bi, hist, R, x, eb, -INFINITY, st, k, &S.tau_key);
     }
+    set_wave_prio(3);
+    int prio = 3;
+    const int pstep = max((qe - qb) / 4, 1);
+    int pmark = qb + pstep;
     for (int q0 = qb; q0 < qe; q0 += WITER) {
+        if (q0 >= pmark) {
+            pmark += pstep;
+            prio = max(prio - 1, 0);
+            set_wave_prio(prio);
+        }
         // two iterations stay in flight while this one is filtered
         f32x4 nx2[U4];
         if (q0 + 3 * WITER <= qe) {
@@ -1418,6 +1740,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             nx1[u] = nx2[u];
         }
     }
+    set_wave_prio(3);
     // resolve the entries still holding upper bounds (below the estimate:
     // dropped, so the count below verifies it)
     if (use_hash) wave_refine(bv, bi, st.cnt, R, tau_est, false);
@@ -1442,6 +1765,153 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         tau_est = -INFINITY;
     }
     }  // attempt
+
+    if (nsl > 1) {
+        // ---- slice: publish the values that can reach the row's pool -------
+        // The slice's own k-th largest Ts is a lower bound of the row's, so
+        // every slice value >= the row threshold is >= Ts.  The list holds
+        // the values passing (ltau, lstrict): >= Ts normally; > t* when a wave
+        // kept only values above its threshold t* >= Ts (ties beyond its
+        // buffer) or when the ties at Ts exceed the list capacity; every value
+        // of the slice when it has fewer than k.
+        int tot_s = 0, strict_s = 0;
+        float tstar_s = -INFINITY;
+#pragma unroll
+        for (int ww = 0; ww < NWAVE; ++ww) {
+            tot_s += S.walive[ww];
+            if (S.wstrict[ww]) {
+                strict_s = 1;
+                tstar_s = fmaxf(tstar_s, S.wtau[ww]);
+            }
+        }
+        float ltau = -INFINITY;
+        bool lstrict = false;
+        float Ts = -INFINITY;
+        if (tot_s >= k) Ts = keyf(block_kth_union<CAPW>(S, k));
+        if (strict_s && (tot_s < k || Ts <= tstar_s)) {
+            ltau = tstar_s;
+            lstrict = true;
+        } else if (tot_s >= k) {
+            ltau = Ts;
+        }
+        const int cnt_w = S.wcnt[w];
+        int mine = 0;
+#pragma unroll
+        for (int r = 0; r < PER; ++r) {
+            const int j = lane + 64 * r;
+            mine += (j < cnt_w) && passes(bv[j], ltau, lstrict);
+        }
+        int n_s = 0;
+        int off = block_excl_scan(mine, n_s, S.wsum[0]);
+        if (n_s > A.lcap) {
+            // more ties at Ts than the list holds (fewer than k values lie above)
+            lstrict = true;
+            mine = 0;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int j = lane + 64 * r;
+                mine += (j < cnt_w) && passes(bv[j], ltau, true);
+            }
+            off = block_excl_scan(mine, n_s, S.wsum[1]);
+        }
+        // (fewer than k values lie above Ts or t*, and lcap > k; a list that
+        // would still not fit is reported instead of written)
+        const bool overflow = n_s > A.lcap;
+        const size_t lo = ((size_t)b * nsl + sl) * A.lcap;
+        // The list and its metadata are written and read with device-coherent
+        // (agent-scope) accesses, and every thread's writes have completed
+        // (vmcnt 0) before the arrival is counted.  Release/acquire fences
+        // would instead write back and invalidate the whole L2 of the XCD for
+        // every slice.
+        if (!overflow) {
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int j = lane + 64 * r;
+                if (j < cnt_w && passes(bv[j], ltau, lstrict)) {
+                    dev_store(A.lst_val + lo + off, bv[j]);
+                    dev_store(A.lst_idx + lo + off, bi[j]);
+                    off++;
+                }
+            }
+        }
+        if (tid == 0) {
+            int *m = reinterpret_cast<int *>(A.lst_meta + (size_t)b * nsl + sl);
+            dev_store(m + 0, overflow ? 0 : n_s);
+            dev_store(m + 1, (int)__float_as_uint(ltau));
+            dev_store(m + 2, lstrict ? 1 : 0);
+            dev_store(m + 3, overflow ? 1 : 0);
+        }
+        wait_stores_done();
+        __syncthreads();
+        if (tid == 0) S.sel_rem = (int)atomicAdd(&A.arrive[b], 1u);
+        __syncthreads();
+        if (S.sel_rem != nsl - 1) return;
+
+        // ---- finisher: gather every slice's list ---------------------------
+        // into the wave-buffer layout (entry i of the concatenation at
+        // cval[i]: wave w holds [w*CAPW, w*CAPW + wcnt[w]))
+        int *offs = reinterpret_cast<int *>(S.u.h.whist[0]);  // nsl + 1 ints
+        float *mtau = reinterpret_cast<float *>(S.u.h.whist[1]);
+        int *mstr = reinterpret_cast<int *>(S.u.h.whist[2]);
+        if (w == 0) {
+            int cnt = 0, st = 0, ov = 0;
+            float tv = -INFINITY;
+            if (lane < nsl) {
+                const int *m = reinterpret_cast<const int *>(A.lst_meta + (size_t)b * nsl + lane);
+                cnt = min(max(dev_load(m + 0), 0), A.lcap);
+                tv = __uint_as_float((uint32_t)dev_load(m + 1));
+                st = dev_load(m + 2);
+                ov = dev_load(m + 3);
+            }
+            const int incl = wave_incl_scan(cnt);
+            if (lane < nsl) {
+                offs[lane] = incl - cnt;
+                mtau[lane] = tv;
+                mstr[lane] = st;
+            }
+            if (lane == 63) offs[MAX_SLICES] = incl;
+            const bool any_ov = __ballot(ov != 0) != 0ull;
+            if (lane == 0) offs[MAX_SLICES + 1] = any_ov ? 1 : 0;
+        }
+        __syncthreads();
+        const int ntot = offs[MAX_SLICES];
+        if (offs[MAX_SLICES + 1]) {
+            // a slice list did not fit: report the row as unsampled
+            if (tid == 0) {
+                A.out_token[b] = -1;
+                if (A.out_ncand) A.out_ncand[b] = -1;
+                A.arrive[b] = 0u;
+            }
+            return;
+        }
+        for (int j = 0; j < nsl; ++j) {
+            const int o = offs[j];
+            const int n = ((j + 1 < nsl) ? offs[j + 1] : ntot) - o;
+            const size_t src = ((size_t)b * nsl + j) * A.lcap;
+            for (int i = tid; i < n; i += WG) {
+                S.cval[o + i] = dev_load(A.lst_val + src + i);
+                S.cidx[o + i] = dev_load(A.lst_idx + src + i);
+            }
+        }
+        if (tid < NWAVE) {
+            const int c = min(max(ntot - tid * CAPW, 0), CAPW);
+            S.wcnt[tid] = c;
+            S.walive[tid] = c;
+            int any = 0;
+            float ts = -INFINITY;
+            if (tid == 0) {
+                for (int j = 0; j < nsl; ++j)
+                    if (mstr[j]) {
+                        any = 1;
+                        ts = fmaxf(ts, mtau[j]);
+                    }
+            }
+            S.wstrict[tid] = any;
+            S.wtau[tid] = ts;
+        }
+        if (tid == 0) A.arrive[b] = 0u;
+        __syncthreads();
+    }
 
     // ---- exact threshold over the union of the wave buffers ---------------
     int total = 0, any_strict = 0;
@@ -1468,7 +1938,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
 
     const bool top_p_on = (A.top_p > 0.0f && A.top_p < 1.0f) && !A.greedy;
-    const float uu = A.uniforms ? A.uniforms[b] : 0.0f;
     int token = V - 1;
     int n_cand = 0, n_kept = 0;
     float sum2 = 0.0f;
@@ -1554,45 +2023,52 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         }
     } else {
         // ---- rescan: the pool is larger than the LDS buffers --------------
+        Nucleus N;
+        N.on = false;
+        N.amax = N.inv = N.plim = 0.0f;
+        N.idlim = 0;
+        bool use_ban = A.any_bans && !A.greedy;
         if (top_p_on) {
-            token = -1;  // not supported: nucleus over a pool above the buffers
-            n_cand = -1;
+            const RescanStats pool = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T,
+                                                                       false, N);
+            N = rescan_nucleus<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, pool.n_cand,
+                                                    pool.max_kept);
+        }
+        RescanStats rs = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, N);
+        if (rs.n_kept == 0 && (use_ban || N.on)) {
+            // restore the whole top-k pool
+            use_ban = false;
+            N.on = false;
+            rs = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false, N);
+        }
+        n_cand = rs.n_cand;
+        n_kept = rs.n_kept;
+        if (A.greedy) {
+            token = rs.first_kept;
+            n_kept = 1;
+            if (A.cand_ld > 0)
+                rescan_write_cands<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false, N, 0.0f,
+                                                        1.0f, true, token, b);
         } else {
-            bool use_ban = A.any_bans && !A.greedy;
-            RescanStats rs = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban);
-            if (use_ban && rs.n_kept == 0) {
-                use_ban = false;  // restore the pool
-                rs = rescan_stats<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false);
-            }
-            n_cand = rs.n_cand;
-            n_kept = rs.n_kept;
-            if (A.greedy) {
-                token = rs.first_kept;
-                n_kept = 1;
-                if (A.cand_ld > 0)
-                    rescan_write_cands<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false, 0.0f,
-                                                            1.0f, true, token, b);
+            const float mx = (rs.max_kept > -1e30f) ? rs.max_kept : -1e30f;
+            sum2 = rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, N, mx,
+                                                          false, 0.0f, nullptr);
+            if (A.variant == LAL_GPU_VARIANT_FILTERED && sum2 <= 0.0f) {
+                token = (rs.max_kept > -1e30f) ? rs.first_max_kept : 0;
             } else {
-                const float mx = (rs.max_kept > -1e30f) ? rs.max_kept : -1e30f;
-                sum2 = rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban,
-                                                              mx, false, 0.0f, nullptr);
-                if (A.variant == LAL_GPU_VARIANT_FILTERED && sum2 <= 0.0f) {
-                    token = (rs.max_kept > -1e30f) ? rs.first_max_kept : 0;
+                const float rr = uu * sum2;
+                if ((A.flags & LAL_GPU_F_DRAW_GPT2) && rr == 0.0f) {
+                    token = 0;
                 } else {
-                    const float rr = uu * sum2;
-                    if ((A.flags & LAL_GPU_F_DRAW_GPT2) && rr == 0.0f) {
-                        token = 0;
-                    } else {
-                        int f = -1;
-                        rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban,
-                                                               mx, true, rr, &f);
-                        token = (f < 0) ? V - 1 : f;
-                    }
+                    int f = -1;
+                    rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, N,
+                                                           mx, true, rr, &f);
+                    token = (f < 0) ? V - 1 : f;
                 }
-                if (A.cand_ld > 0)
-                    rescan_write_cands<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, mx,
-                                                            sum2, false, token, b);
             }
+            if (A.cand_ld > 0)
+                rescan_write_cands<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, N, mx,
+                                                        sum2, false, token, b);
         }
     }
 
@@ -1861,7 +2337,7 @@ __global__ void expf_check_kernel(uint32_t first_hi, int nhi, uint64_t *out)
     uint64_t h = 0;
     for (uint32_t lo = threadIdx.x; lo < 65536u; lo += blockDim.x) {
         const uint32_t ux = (hi << 16) | lo;
-        const float r = glibc_expf(__uint_as_float(ux));
+        const float r = glibc_expf(__uint_as_float(ux), kExp2Tab);
         uint32_t rb = __float_as_uint(r);
         if (r != r) rb = 0x7fc00000u;
         h += mix64(((uint64_t)ux << 32) | rb);
@@ -1886,6 +2362,13 @@ struct lal_gpu_ctx {
     int device;
     int max_batch;
     int max_vocab;
+    // slice lists (see KArgs): max_batch x FLAT_MAX entries, metadata for up
+    // to MAX_SLICES slices per row, one arrival counter per row (zeroed here,
+    // reset by every row's finisher)
+    float *lst_val;
+    int *lst_idx;
+    int4 *lst_meta;
+    unsigned *arrive;
 };
 
 static thread_local hipError_t g_last_hip = hipSuccess;
@@ -1946,11 +2429,50 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     c->device = device;
     c->max_batch = max_batch;
     c->max_vocab = max_vocab;
+    const size_t nl = (size_t)max_batch * FLAT_MAX;
+    hipError_t e = hipMalloc((void **)&c->lst_val, nl * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->lst_idx, nl * sizeof(int));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->lst_meta, (size_t)max_batch * MAX_SLICES * sizeof(int4));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->arrive, (size_t)max_batch * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMemset(c->arrive, 0, (size_t)max_batch * sizeof(unsigned));
+    if (e != hipSuccess) {
+        lal_gpu_destroy(c);
+        return e == hipErrorOutOfMemory ? LAL_GPU_E_NOMEM : hip_fail(e);
+    }
     *out = c;
     return LAL_GPU_OK;
 }
 
-void lal_gpu_destroy(lal_gpu_ctx *ctx) { free(ctx); }
+void lal_gpu_destroy(lal_gpu_ctx *ctx)
+{
+    if (!ctx) return;
+    int cur = -1;
+    if (hipGetDevice(&cur) == hipSuccess && cur != ctx->device) (void)hipSetDevice(ctx->device);
+    if (ctx->lst_val) (void)hipFree(ctx->lst_val);
+    if (ctx->lst_idx) (void)hipFree(ctx->lst_idx);
+    if (ctx->lst_meta) (void)hipFree(ctx->lst_meta);
+    if (ctx->arrive) (void)hipFree(ctx->arrive);
+    if (cur >= 0 && cur != ctx->device) (void)hipSetDevice(cur);
+    free(ctx);
+}
+
+// Slices per row.  A slice costs a fixed setup and finish on top of its
+// streaming, so rows are split only to give a small batch enough workgroups
+// (about one per slot: 4 per CU): slices of at least 64 Ki elements, or
+// 16 Ki for a batch of at most 4 rows (latency); list capacity above k.
+constexpr int TARGET_WGS = 1024;
+static int choose_slices(int batch, int vocab, int k_eff, int flat)
+{
+    if (const char *env = getenv("LAL_GPU_SLICES")) {
+        const int n = atoi(env);
+        if (n >= 1) return std::min(std::min(n, MAX_SLICES), std::max(1, flat / (k_eff + 1)));
+    }
+    const int min_len = (batch <= 4) ? 16384 : 65536;
+    int n = (TARGET_WGS + batch - 1) / batch;
+    n = std::min(n, std::max(1, vocab / min_len));
+    n = std::min(n, std::max(1, flat / (k_eff + 1)));
+    return std::max(1, std::min(n, MAX_SLICES));
+}
 
 int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_params *p,
                    const lal_gpu_sample_io *io, void *stream)
@@ -2024,8 +2546,17 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     }
 
     hipStream_t s = (hipStream_t)stream;
-    const dim3 grid(batch), block(WG);
     const bool small = greedy || p->top_k <= K_SMALL_MAX;
+    const int k_eff = greedy ? 1 : std::min(p->top_k, vocab);
+    const int flat = NWAVE * (small ? CAPW_SMALL : CAPW_LARGE);
+    A.batch = batch;
+    A.nslice = choose_slices(batch, vocab, k_eff, flat);
+    A.lcap = flat / A.nslice;
+    A.lst_val = ctx->lst_val;
+    A.lst_idx = ctx->lst_idx;
+    A.lst_meta = ctx->lst_meta;
+    A.arrive = ctx->arrive;
+    const dim3 grid((unsigned)(((batch + 7) / 8) * 8 * A.nslice)), block(WG);
 #define LAL_LAUNCH(HB, HA)                                                                   \
     do {                                                                                     \
         if (small)                                                                           \

@@ -235,3 +235,59 @@ def test_expf_matches_glibc_exhaustively(dev, orc):
     c = orc.expf_checksums(0, n)
     bad = np.nonzero(g != c)[0]
     assert len(bad) == 0, f"expf differs from glibc in chunks {bad[:10]} (inputs hi<<16)"
+
+
+# ---------------------------------------------------------------------------
+# rows split into slices (one workgroup each, lists merged by the last slice):
+# the result must not depend on the split
+# ---------------------------------------------------------------------------
+@pytest.fixture
+def slices(monkeypatch):
+    def set_slices(n):
+        monkeypatch.setenv("LAL_GPU_SLICES", str(n))
+    yield set_slices
+
+
+@pytest.mark.parametrize("nsl", [2, 3, 7, 16])
+def test_sliced_rows_match_oracle(run, orc, slices, nsl):
+    slices(nsl)
+    B, V = 8, 40009
+    kinds = ["gauss", "ties", "zipf", "outliers", "neginf", "signed_zero", "ascending", "huge"]
+    x = np.stack([synth.make_row(kinds[b], 900 + b, V) for b in range(B)])
+    hist = synth.history(14, B, 48, V, with_invalid=True)
+    u = np.array([0.0, 1.0, 0.5, 0.25, 0.999, 1e-7, 0.75, 0.3], np.float32)
+    for k, top_p, variant in ((1, 0.0, 0), (7, 0.0, 1), (40, 0.9, 0), (50, 0.5, 1), (300, 0.0, 0),
+                              (512, 0.95, 1)):
+        kw = dict(T=0.9, k=k, top_p=top_p, pen=1.15, variant=variant, hist=hist, u=u, cand_ld=600,
+                  ban_last=1, ban_repeat=3, mask_recent=2)
+        log(f"slices {nsl} k {k} top_p {top_p} variant {variant}")
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=600)
+
+
+@pytest.mark.parametrize("nsl", [2, 5])
+def test_sliced_qwen7b_batch(dev, run, orc, slices, nsl):
+    """The 1024 x 152064 top-k/top-p step with every row split."""
+    slices(nsl)
+    B = 1024
+    x = gpu_logits(dev, "zipf", B, V7B, V7B, 21)
+    hist = synth.history(22, B, 256, V7B)
+    u = orc.uniforms(23, B)
+    kw = dict(T=0.8, k=50, top_p=0.9, pen=1.1, hist=hist, u=u, cand_ld=64)
+    assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=64)
+
+
+@pytest.mark.parametrize("nsl", [1, 3])
+def test_pool_above_buffers_with_top_p(run, orc, slices, nsl):
+    """Constant rows: the pool is the whole row (ties beyond every buffer), so
+    the nucleus is formed by an id-order rescan of the row."""
+    slices(nsl)
+    B, V = 4, 30011
+    x = np.stack([synth.make_row("const", 5 + b, V) for b in range(B)])
+    x[1, 100:200] += np.float32(0.5)   # a few larger values ahead of the tie group
+    x[2, ::7] = np.float32(-np.inf)
+    hist = synth.history(15, B, 16, V)
+    u = np.array([0.0, 0.3, 0.77, 1.0], np.float32)
+    for k, top_p in ((40, 0.9), (512, 0.3), (1, 0.5), (300, 0.999)):
+        kw = dict(T=0.8, k=k, top_p=top_p, pen=1.1, hist=hist, u=u, cand_ld=64, ban_last=1)
+        log(f"rescan top-p slices {nsl} k {k} p {top_p}")
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=64)
