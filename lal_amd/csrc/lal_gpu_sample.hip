@@ -144,36 +144,66 @@ __device__ __forceinline__ void wave_sync()
     __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+// Wave64 scans and reductions with DPP row shifts and row broadcasts (VALU
+// only, no LDS round trips): within each row of 16 lanes by row_shr 1, 2, 4,
+// 8, then row 0's total into row 1 (row_bcast:15, rows 1 and 3) and rows 0-1's
+// total into rows 2-3 (row_bcast:31).  Lanes without a source keep `old`, the
+// identity.  Reductions return lane 63's value (uniform).
+#define LAL_DPP_SCAN(OP, T, IDENT, TOI, FROMI)                                            \
+    do {                                                                                  \
+        v = OP(v, FROMI(__builtin_amdgcn_update_dpp(TOI(IDENT), TOI(v), 0x111, 0xf, 0xf, false))); \
+        v = OP(v, FROMI(__builtin_amdgcn_update_dpp(TOI(IDENT), TOI(v), 0x112, 0xf, 0xf, false))); \
+        v = OP(v, FROMI(__builtin_amdgcn_update_dpp(TOI(IDENT), TOI(v), 0x114, 0xf, 0xf, false))); \
+        v = OP(v, FROMI(__builtin_amdgcn_update_dpp(TOI(IDENT), TOI(v), 0x118, 0xf, 0xf, false))); \
+        v = OP(v, FROMI(__builtin_amdgcn_update_dpp(TOI(IDENT), TOI(v), 0x142, 0xa, 0xf, false))); \
+        v = OP(v, FROMI(__builtin_amdgcn_update_dpp(TOI(IDENT), TOI(v), 0x143, 0xc, 0xf, false))); \
+    } while (0)
+
+__device__ __forceinline__ int op_add(int a, int b) { return a + b; }
+__device__ __forceinline__ int op_min(int a, int b) { return min(a, b); }
+__device__ __forceinline__ unsigned op_maxu(unsigned a, unsigned b) { return max(a, b); }
+__device__ __forceinline__ unsigned op_minu(unsigned a, unsigned b) { return min(a, b); }
+__device__ __forceinline__ float op_fmax(float a, float b) { return fmaxf(a, b); }
+__device__ __forceinline__ int id_i(int x) { return x; }
+__device__ __forceinline__ int u2i(unsigned x) { return (int)x; }
+__device__ __forceinline__ unsigned i2u(int x) { return (unsigned)x; }
+__device__ __forceinline__ int f2i(float x) { return __float_as_int(x); }
+__device__ __forceinline__ float i2f(int x) { return __int_as_float(x); }
+
 __device__ __forceinline__ int wave_incl_scan(int v)
 {
-    const int lane = lane_id();
-#pragma unroll
-    for (int d = 1; d < 64; d <<= 1) {
-        int t = __shfl_up(v, d, 64);
-        if (lane >= d) v += t;
-    }
+    LAL_DPP_SCAN(op_add, int, 0, id_i, id_i);
     return v;
 }
 
 __device__ __forceinline__ float wave_max(float v)
 {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v = fmaxf(v, __shfl_xor(v, d, 64));
-    return v;
+    LAL_DPP_SCAN(op_fmax, float, -INFINITY, f2i, i2f);
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 63));
 }
 
 __device__ __forceinline__ int wave_min(int v)
 {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v = min(v, __shfl_xor(v, d, 64));
-    return v;
+    LAL_DPP_SCAN(op_min, int, INT_MAX, id_i, id_i);
+    return __builtin_amdgcn_readlane(v, 63);
 }
 
 __device__ __forceinline__ int wave_sum(int v)
 {
-#pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
-    return v;
+    LAL_DPP_SCAN(op_add, int, 0, id_i, id_i);
+    return __builtin_amdgcn_readlane(v, 63);
+}
+
+__device__ __forceinline__ unsigned wave_max_u(unsigned v)
+{
+    LAL_DPP_SCAN(op_maxu, unsigned, 0u, u2i, i2u);
+    return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
+}
+
+__device__ __forceinline__ unsigned wave_min_u(unsigned v)
+{
+    LAL_DPP_SCAN(op_minu, unsigned, 0xFFFFFFFFu, u2i, i2u);
+    return (unsigned)__builtin_amdgcn_readlane((int)v, 63);
 }
 
 __device__ __forceinline__ int readlane_i(int v, int l) { return __builtin_amdgcn_readlane(v, l); }
@@ -520,36 +550,6 @@ __device__ __forceinline__ float exact_value(const RowCtx &R, int e, float yhat)
     return yhat;
 }
 
-// Sort one key per lane descending (bitonic network over the wave).
-__device__ __forceinline__ uint32_t wave_sort_desc(uint32_t key)
-{
-    const int lane = lane_id();
-#pragma unroll
-    for (int size = 2; size <= 64; size <<= 1) {
-#pragma unroll
-        for (int stride = size >> 1; stride > 0; stride >>= 1) {
-            const uint32_t other = (uint32_t)__shfl_xor((int)key, stride, 64);
-            const bool take_max = (((lane & size) == 0) == ((lane & stride) == 0));
-            key = take_max ? max(key, other) : min(key, other);
-        }
-    }
-    return key;
-}
-
-// Top 64 of two descending-sorted lane vectors a, b, sorted descending:
-// max(a_i, b_{63-i}) is bitonic, a half-cleaner cascade sorts it.
-__device__ __forceinline__ uint32_t wave_merge_top_desc(uint32_t a, uint32_t b)
-{
-    const int lane = lane_id();
-    uint32_t key = max(a, (uint32_t)__shfl((int)b, 63 - lane, 64));
-#pragma unroll
-    for (int stride = 32; stride > 0; stride >>= 1) {
-        const uint32_t other = (uint32_t)__shfl_xor((int)key, stride, 64);
-        key = ((lane & stride) == 0) ? max(key, other) : min(key, other);
-    }
-    return key;
-}
-
 // k-th largest of the 64 lane keys (1 <= k <= 64), bit by bit: the largest K
 // with at least k keys >= K.  Ballot counts only; wave-synchronous.
 __device__ __forceinline__ uint32_t wave_kth_lane_key(uint32_t key, int k)
@@ -793,23 +793,56 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
 template <int CAPW, class SM>
 __device__ __forceinline__ uint32_t block_kth_union(SM &S, int k)
 {
+    constexpr int PK = CAPW / 64;  // entries per lane of its own wave's buffer
     unsigned *hist = S.u.h.whist[0];
     const int w = wave_id(), lane = lane_id();
     const int cnt = S.wcnt[w];
     const float *bv = S.cval + w * CAPW;
-    uint32_t prefix = 0, pmask = 0;
+    // keys of the live entries (0 = none), and their range over the block
+    uint32_t key[PK];
+    uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
+#pragma unroll
+    for (int r = 0; r < PK; ++r) {
+        const int j = lane + 64 * r;
+        const float v = (j < cnt) ? bv[j] : NAN;
+        key[r] = (v == v) ? fkey(v) : 0u;
+        if (key[r]) {
+            kmax = max(kmax, key[r]);
+            kmin = min(kmin, key[r]);
+        }
+    }
+    kmax = (uint32_t)wave_max_u(kmax);
+    kmin = (uint32_t)wave_min_u(kmin);
+    __syncthreads();
+    if (lane == 0) {
+        S.redi[w] = (int)kmax;
+        S.redi2[w] = (int)kmin;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ww = 0; ww < NWAVE; ++ww) {
+        kmax = max(kmax, (uint32_t)S.redi[ww]);
+        kmin = min(kmin, (uint32_t)S.redi2[ww]);
+    }
+    if (kmin >= kmax) {  // every live key is equal (k <= count)
+        __syncthreads();
+        return kmax;
+    }
+    // the bits above the first one where the keys differ are common: select
+    // from there, 8 bits per pass
+    const int L = __builtin_clz(kmin ^ kmax);
+    uint32_t pmask = L ? ~0u << (32 - L) : 0u;
+    uint32_t prefix = kmax & pmask;
     int rem = k;
-    for (int pass = 0; pass < 4; ++pass) {
-        const int shift = 24 - 8 * pass;
+    for (int hi = 31 - L; hi >= 0; hi -= 8) {
+        const int lo = max(hi - 7, 0);
+        const uint32_t dmask = (hi - lo == 31) ? ~0u : ((1u << (hi - lo + 1)) - 1u);
         __syncthreads();
         hist[threadIdx.x] = 0;
         __syncthreads();
-        for (int j = lane; j < cnt; j += 64) {
-            const float v = bv[j];
-            if (v != v) continue;
-            const uint32_t key = fkey(v);
-            if ((key & pmask) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
-        }
+#pragma unroll
+        for (int r = 0; r < PK; ++r)
+            if (key[r] && (key[r] & pmask) == prefix) atomicAdd(&hist[(key[r] >> lo) & dmask], 1u);
         __syncthreads();
         if (w == 0) {
             const int b0 = 255 - 4 * lane;
@@ -828,8 +861,8 @@ __device__ __forceinline__ uint32_t block_kth_union(SM &S, int k)
             }
         }
         __syncthreads();
-        prefix |= (uint32_t)S.sel_digit << shift;
-        pmask |= 0xFFu << shift;
+        prefix |= (uint32_t)S.sel_digit << lo;
+        pmask |= dmask << lo;
         rem = S.sel_rem;
     }
     __syncthreads();
@@ -1609,15 +1642,20 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const int ks = (int)ceilf(lam + 6.0f * sqrtf(lam) + 6.0f);
         if (!A.greedy && nsmp > 0 && ks <= 64) {
             unsigned *tmp = S.u.h.whist[0];  // 4 x 64 keys
-            const uint32_t key = wave_sort_desc((lm == lm && lm > -INFINITY) ? fkey(lm) : 0u);
-            tmp[w * 64 + lane] = key;
+            tmp[tid] = (lm == lm && lm > -INFINITY) ? fkey(lm) : 0u;
             __syncthreads();
             if (w == 0) {
-                const uint32_t a = wave_merge_top_desc(tmp[lane], tmp[64 + lane]);
-                const uint32_t c2 = wave_merge_top_desc(tmp[128 + lane], tmp[192 + lane]);
-                const uint32_t top = wave_merge_top_desc(a, c2);
-                const uint32_t kk = (uint32_t)readlane_i((int)top, ks - 1);
-                if (lane == 0) S.sel_rem = (int)kk;
+                // the ks-th largest of the 256 keys, bit by bit (ballot counts)
+                const uint32_t k0 = tmp[lane], k1 = tmp[64 + lane], k2 = tmp[128 + lane],
+                               k3 = tmp[192 + lane];
+                uint32_t K = 0u;
+                for (int bit = 31; bit >= 0; --bit) {
+                    const uint32_t cand = K | (1u << bit);
+                    const int c = __popcll(__ballot(k0 >= cand)) + __popcll(__ballot(k1 >= cand)) +
+                                  __popcll(__ballot(k2 >= cand)) + __popcll(__ballot(k3 >= cand));
+                    if (c >= ks) K = cand;
+                }
+                if (lane == 0) S.sel_rem = (int)K;
             }
             __syncthreads();
             const uint32_t kk = (uint32_t)S.sel_rem;
