@@ -224,20 +224,6 @@ __device__ __forceinline__ T dev_load(const T *p)
 {
     return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
-// Wave issue priority (0..3).  Streaming waves lower theirs as they progress,
-// so a wave that is behind (e.g. the youngest workgroup on a CU, which the
-// age-ordered arbiter serves last) is served first; latency-bound phases run
-// at the top level.
-__device__ __forceinline__ void set_wave_prio(int level)
-{
-    switch (level) {
-    case 0: __builtin_amdgcn_s_setprio(0); break;
-    case 1: __builtin_amdgcn_s_setprio(1); break;
-    case 2: __builtin_amdgcn_s_setprio(2); break;
-    default: __builtin_amdgcn_s_setprio(3); break;
-    }
-}
-
 // Wait until this thread's outstanding memory operations have completed.
 __device__ __forceinline__ void wait_stores_done() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
@@ -1549,6 +1535,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     const int h1 = (tid + WG < nh) ? hrow[tid + WG] : -1;
     const int bid = (tid < A.n_ban) ? A.ban_ids[tid] : -1;
     const float uu = (A.uniforms && !A.greedy) ? A.uniforms[b] : 0.0f;
+    const uint64_t xtab = (tid < 32) ? kExp2Tab[tid] : 0ull;
 
     const RowGeo g = row_geo(row, V);
     const int k = A.greedy ? 1 : min(max(A.k, 1), V);
@@ -1580,12 +1567,42 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
     }
 
-    // ---- setup: hash of history / ban ids -------------------------------
+    // ---- setup: hash of history / ban ids, and the threshold estimate ----
+    // tau_est = the ks-th largest of the per-thread maxima of the sampled
+    // upper bounds (a subset of the sample, so no larger than the sample's
+    // ks-th largest); ks is chosen so that with the sampling fraction f the
+    // sample holds fewer than ks of the row's top-k except with negligible
+    // probability.  It is verified after streaming (>= k captured values) and
+    // the row is streamed again without it when the check fails.
+    unsigned *skeys = S.u.h.whist[0];  // 4 x 64 sample keys
+    int nsmp = 0;                      // sampled positions (closed form)
+    for (int jb = 0; jb < SR * NWAVE; ++jb) {
+        const int st0 = sb + jb * SBLK;
+        if (st0 < se) nsmp += 4 * min(64, se - st0);
+    }
+    const float lam = (float)k * (float)nsmp / (float)max(vlen, 1);
+    const int ks = (int)ceilf(lam + 6.0f * sqrtf(lam) + 6.0f);
+    const bool use_est = !A.greedy && nsmp > 0 && ks <= 64;
+    {
+        float lm = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < SR; ++r) {
+            const int sidx = tid + WG * r;
+            const int q = sb + (sidx >> 6) * SBLK + (sidx & 63);
+            if (q < se) {
+#pragma unroll
+                for (int c = 0; c < 4; ++c)
+                    lm = fmaxf(lm, upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, g.head + 4 * q + c,
+                                                                   smp[r][c]));
+            }
+        }
+        skeys[tid] = (lm == lm && lm > -INFINITY) ? fkey(lm) : 0u;
+    }
     for (int s = tid; s < HSLOTS; s += WG) {
         S.hkey[s] = -1;
         S.hinfo[s] = 0;
     }
-    if (tid < 32) S.exptab[tid] = kExp2Tab[tid];
+    if (tid < 32) S.exptab[tid] = xtab;
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -1599,7 +1616,25 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         hash_insert(S.hkey, S.hinfo, t, A.apply_pen ? 1 : 0, flags);
     }
     if (bid >= 0 && bid < V) hash_insert(S.hkey, S.hinfo, bid, 0, HF_BAN);
+    if (use_est && w == 0) {
+        // the ks-th largest of the 256 keys, bit by bit (ballot counts)
+        const uint32_t k0 = skeys[lane], k1 = skeys[64 + lane], k2 = skeys[128 + lane],
+                       k3 = skeys[192 + lane];
+        uint32_t K = 0u;
+        for (int bit = 31; bit >= 0; --bit) {
+            const uint32_t cand = K | (1u << bit);
+            const int c = __popcll(__ballot(k0 >= cand)) + __popcll(__ballot(k1 >= cand)) +
+                          __popcll(__ballot(k2 >= cand)) + __popcll(__ballot(k3 >= cand));
+            if (c >= ks) K = cand;
+        }
+        if (lane == 0) S.sel_rem = (int)K;
+    }
     __syncthreads();
+    float tau_est = -INFINITY;
+    if (use_est) {
+        const uint32_t kk = (uint32_t)S.sel_rem;
+        if (kk) tau_est = keyf(kk);
+    }
     const bool use_hash = (nh > 0) || (A.n_ban > 0);
     RowCtx R;
     R.row = row;
@@ -1611,57 +1646,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     R.has_bias = HAS_BIAS;
     R.has_allow = HAS_ALLOW;
     R.use_hash = use_hash;
-
-    // ---- threshold estimate from the sample ------------------------------
-    // tau_est = the ks-th largest of the per-thread maxima of the sampled
-    // upper bounds (a subset of the sample, so no larger than the sample's
-    // ks-th largest); ks is chosen so that with the sampling fraction f the
-    // sample holds fewer than ks of the row's top-k except with negligible
-    // probability.  It is verified after streaming (>= k captured values) and
-    // the row is streamed again without it when the check fails.
-    float tau_est = -INFINITY;
-    {
-        float lm = -INFINITY;
-        int nvalid = 0;
-#pragma unroll
-        for (int r = 0; r < SR; ++r) {
-            const int sidx = tid + WG * r;
-            const int q = sb + (sidx >> 6) * SBLK + (sidx & 63);
-            if (q < se) {
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const float v = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, g.head + 4 * q + c,
-                                                                     smp[r][c]);
-                    lm = fmaxf(lm, v);
-                    nvalid++;
-                }
-            }
-        }
-        const int nsmp = block_sum(S, nvalid);
-        const float lam = (float)k * (float)nsmp / (float)max(vlen, 1);
-        const int ks = (int)ceilf(lam + 6.0f * sqrtf(lam) + 6.0f);
-        if (!A.greedy && nsmp > 0 && ks <= 64) {
-            unsigned *tmp = S.u.h.whist[0];  // 4 x 64 keys
-            tmp[tid] = (lm == lm && lm > -INFINITY) ? fkey(lm) : 0u;
-            __syncthreads();
-            if (w == 0) {
-                // the ks-th largest of the 256 keys, bit by bit (ballot counts)
-                const uint32_t k0 = tmp[lane], k1 = tmp[64 + lane], k2 = tmp[128 + lane],
-                               k3 = tmp[192 + lane];
-                uint32_t K = 0u;
-                for (int bit = 31; bit >= 0; --bit) {
-                    const uint32_t cand = K | (1u << bit);
-                    const int c = __popcll(__ballot(k0 >= cand)) + __popcll(__ballot(k1 >= cand)) +
-                                  __popcll(__ballot(k2 >= cand)) + __popcll(__ballot(k3 >= cand));
-                    if (c >= ks) K = cand;
-                }
-                if (lane == 0) S.sel_rem = (int)K;
-            }
-            __syncthreads();
-            const uint32_t kk = (uint32_t)S.sel_rem;
-            if (kk) tau_est = keyf(kk);
-        }
-    }
 
     float *bv = S.cval + w * CAPW;
     int *bi = S.cidx + w * CAPW;
@@ -1695,16 +1679,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         if (e >= 0) x[0] = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
         wave_offer<1, CAPW>(bv, bi, hist, R, x, eb, -INFINITY, st, k, &S.tau_key);
     }
-    set_wave_prio(3);
-    int prio = 3;
-    const int pstep = max((qe - qb) / 4, 1);
-    int pmark = qb + pstep;
     for (int q0 = qb; q0 < qe; q0 += WITER) {
-        if (q0 >= pmark) {
-            pmark += pstep;
-            prio = max(prio - 1, 0);
-            set_wave_prio(prio);
-        }
         // two iterations stay in flight while this one is filtered
         f32x4 nx2[U4];
         if (q0 + 3 * WITER <= qe) {
@@ -1778,7 +1753,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             nx1[u] = nx2[u];
         }
     }
-    set_wave_prio(3);
     // resolve the entries still holding upper bounds (below the estimate:
     // dropped, so the count below verifies it)
     if (use_hash) wave_refine(bv, bi, st.cnt, R, tau_est, false);
@@ -2012,32 +1986,59 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         }
         __syncthreads();
         n_cand = nc;
-        int rk[PER];
-#pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            const int j = tid + r * WG;
-            rk[r] = -1;
-            if (j < nc) {
-                rv[r] = S.cval[j];
-                ri[r] = S.cidx[j];
+        if (nc <= 64) {
+            // one candidate per lane of wave 0; ranks against the ids read four
+            // at a time (no barrier)
+            if (w == 0) {
+                const float myv = (lane < nc) ? S.cval[lane] : 0.0f;
+                const int myid = (lane < nc) ? S.cidx[lane] : INT_MAX;
                 int rank = 0;
-                for (int q = 0; q < nc; ++q) rank += (S.cidx[q] < ri[r]);
-                rk[r] = rank;
-            }
-        }
-        __syncthreads();
 #pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            if (rk[r] >= 0) {
-                S.cval[rk[r]] = rv[r];
-                S.cidx[rk[r]] = ri[r];
+                for (int q4 = 0; q4 < 16; ++q4) {
+                    if (4 * q4 < nc) {
+                        const int4 v = reinterpret_cast<const int4 *>(S.cidx)[q4];
+                        rank += (4 * q4 + 0 < nc && v.x < myid);
+                        rank += (4 * q4 + 1 < nc && v.y < myid);
+                        rank += (4 * q4 + 2 < nc && v.z < myid);
+                        rank += (4 * q4 + 3 < nc && v.w < myid);
+                    }
+                }
+                wave_sync();
+                if (lane < nc) {
+                    S.cval[rank] = myv;
+                    S.cidx[rank] = myid;
+                }
+                wave_sync();
             }
+        } else {
+            int rk[PER];
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int j = tid + r * WG;
+                rk[r] = -1;
+                if (j < nc) {
+                    rv[r] = S.cval[j];
+                    ri[r] = S.cidx[j];
+                    int rank = 0;
+                    for (int q = 0; q < nc; ++q) rank += (S.cidx[q] < ri[r]);
+                    rk[r] = rank;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                if (rk[r] >= 0) {
+                    S.cval[rk[r]] = rv[r];
+                    S.cidx[rk[r]] = ri[r];
+                }
+            }
+            __syncthreads();
         }
-        __syncthreads();
 
         if (nc == 0) {
             token = V - 1;
         } else if (A.greedy) {
+            if (nc <= 64) __syncthreads();  // wave 0 sorted the pool
             token = S.cidx[0];
             n_kept = 1;
             for (int j = tid; j < nc && j < A.cand_ld; j += WG) {
