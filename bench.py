@@ -37,6 +37,16 @@ WORKLOADS = {
     "constrained": dict(B=512, V=152064, kind="gauss", T=0.7, k=40, top_p=0.0, pen=1.0, H=16,
                         allow=0.05, bias_nnz=2000, mask_recent=16),
 }
+# Q8 LM head + sampling: hidden [B, 3584] ~ N(0,1) quantized per row, W int8
+# [152064, 3584] uniform in [-127, 127], sw ~ U(0.001, 0.02); then penalty 1.1
+# over 64 ids, T 0.7, top-k 40.  A step is quantize + LM head + sample.
+for _b in (1, 16, 64):
+    WORKLOADS[f"q8_lm_head_sample_b{_b}"] = dict(B=_b, V=152064, kind="lmhead", n=3584, T=0.7, k=40,
+                                                top_p=0.0, pen=1.1, H=64)
+
+
+def lm_head_weight_bytes(w):
+    return w["V"] * w["n"] + 4 * w["V"]
 
 
 def algorithmic_bytes_per_row(w):
@@ -50,6 +60,9 @@ def algorithmic_bytes_per_row(w):
 
 
 def algorithmic_bytes_per_step(w):
+    if w["kind"] == "lmhead":
+        # W and its scales once, each row's hidden state and history, the id
+        return lm_head_weight_bytes(w) + w["B"] * (4 * w["n"] + 4 * w["H"] + 4 + 4)
     b = w["B"] * algorithmic_bytes_per_row(w)
     if w.get("bias_nnz"):
         b += 4 * w["V"]
@@ -62,7 +75,18 @@ class Inputs:
         lib = dev.lib
         B, V, H = w["B"], w["V"], w["H"]
         self.logits = dev.alloc(4 * B * V)
-        if w["kind"] == "zipf":
+        self.lmhead = None
+        if w["kind"] == "lmhead":
+            n = w["n"]
+            self.lmhead = dict(n=n, w=dev.alloc(V * n), sw=dev.alloc(4 * V), x=dev.alloc(4 * B * n),
+                               xq=dev.alloc(B * n), sx=dev.alloc(4 * B))
+            L = self.lmhead
+            abi.check(lib.lal_gpu_synth_int8(abi.ptr(L["w"]), V * n, seed + 5, -127, 127, dev.stream), "w")
+            abi.check(lib.lal_gpu_synth_uniform(abi.ptr(L["sw"]), V, seed + 6, C.c_float(0.001),
+                                                C.c_float(0.02), dev.stream), "sw")
+            abi.check(lib.lal_gpu_synth_normal(abi.ptr(L["x"]), B * n, seed + 7, C.c_float(1.0), dev.stream),
+                      "x")
+        elif w["kind"] == "zipf":
             abi.check(lib.lal_gpu_synth_zipf(abi.ptr(self.logits), B, V, V, seed, C.c_float(1.1),
                                              C.c_float(0.3), dev.stream), "synth")
         else:
@@ -157,6 +181,37 @@ def cpu_baseline(w, dev, inputs, target_s=4.0):
             "one_thread_rows_per_s": rows_s1}
 
 
+def cpu_baseline_lmhead(w, dev, inputs):
+    """The CPU oracle for one row of the Q8 LM head + sampling step: quantize
+    the hidden state, the int8 LM head over the full vocabulary (OpenMP over
+    vocab rows, as tools/server/qwen7b_server.c:833-845 splits it), then the
+    sampler; timed on this host's cores."""
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from oracle_lib import Oracle, make_params as oparams
+    orc = Oracle()
+    L = inputs.lmhead
+    V, n = w["V"], L["n"]
+    W = L["w"].download((V, n), np.int8)
+    sw = L["sw"].download(V, np.float32)
+    x = L["x"].download((w["B"], n), np.float32)[0].copy()
+    h = inputs.hist.download((w["B"], w["H"]), np.int32)[:1].copy()
+    u = inputs.u.download(w["B"], np.float32)[:1].copy()
+    p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"])
+    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
+    done, t0 = 0, time.perf_counter()
+    while True:
+        sx, xq = orc.quantize_x(x, 0)
+        logits = orc.lm_head(xq, sx, W, sw, nthreads=threads)[None, :]
+        orc.sample_batch(logits, p, hist=h, uniforms=u, nthreads=1)
+        done += 1
+        el = time.perf_counter() - t0
+        if el >= 4.0 or done >= 32:
+            break
+    return {"value": done / el, "unit": "rows/s", "cores": threads, "kind": "port",
+            "sample": f"{done} rows (row 0 of the batch, repeated): quantize, LM head over "
+                      f"{V} x {n} int8 with OpenMP over vocab rows, sampler"}
+
+
 def read_traffic(name):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary."""
     path = os.path.join(ROOT, "profiles", f"pmc_sample_rows_{name}.txt")
@@ -192,19 +247,31 @@ def main():
     from lal_amd import abi
     w = WORKLOADS[args.workload]
     dev = abi.Device(0, max_batch=w["B"], max_vocab=w["V"])
-    sets = [Inputs(dev, w, 1000 + 17 * i) for i in range(max(1, args.sets))]
+    nsets = 1 if w["kind"] == "lmhead" else max(1, args.sets)  # W alone exceeds the 256 MB cache
+    sets = [Inputs(dev, w, 1000 + 17 * i) for i in range(nsets)]
     ios = [s.io(w) for s in sets]
     params = params_for(w)
 
-    for i in range(args.warmup):
+    def step(i):
+        inp = sets[i % len(sets)]
+        if inp.lmhead is not None:
+            L = inp.lmhead
+            abi.check(dev.lib.lal_gpu_quantize_x(dev.ctx, abi.ptr(L["x"]), w["B"], L["n"], 0, abi.ptr(L["xq"]),
+                                                 abi.ptr(L["sx"]), dev.stream), "quantize_x")
+            abi.check(dev.lib.lal_gpu_lm_head_q8(dev.ctx, abi.ptr(L["xq"]), abi.ptr(L["sx"]), w["B"], L["n"],
+                                                 abi.ptr(L["w"]), abi.ptr(L["sw"]), w["V"],
+                                                 abi.ptr(inp.logits), w["V"], dev.stream), "lm_head_q8")
         dev.sample(w["B"], w["V"], params, ios[i % len(ios)])
+
+    for i in range(args.warmup):
+        step(i)
     dev.sync()
     abi.check(dev.lib.lal_gpu_device_sync(), "sync")
     e0, e1 = dev.event(), dev.event()
     t0 = time.perf_counter()
     dev.record(e0)
     for i in range(args.steps):
-        dev.sample(w["B"], w["V"], params, ios[i % len(ios)])
+        step(i)
     dev.record(e1)
     dev.sync()
     abi.check(dev.lib.lal_gpu_device_sync(), "sync")
@@ -232,6 +299,8 @@ def main():
         "config": {"workload": args.workload, "batch": w["B"], "vocab": w["V"],
                    "logits": w["kind"], "temperature": w["T"], "top_k": w["k"],
                    "top_p": w["top_p"], "rep_penalty": w["pen"], "history_ids": w["H"],
+                   **({"hidden": w["n"], "lm_head": "int8 [152064, 3584] + per-row fp32 scales"}
+                      if w["kind"] == "lmhead" else {}),
                    "rotating_input_sets": len(sets),
                    "live_input_bytes": len(sets) * 4 * w["B"] * w["V"],
                    **({"allow_p": w["allow"], "bias_nnz": w["bias_nnz"],
@@ -243,7 +312,10 @@ def main():
         "wall_s_timed_region": wall,
     }
     if not args.no_cpu_baseline:
-        out["cpu_baseline"] = cpu_baseline(w, dev, sets[0])
+        if w["kind"] == "lmhead":
+            out["cpu_baseline"] = cpu_baseline_lmhead(w, dev, sets[0])
+        else:
+            out["cpu_baseline"] = cpu_baseline(w, dev, sets[0])
     else:
         out["cpu_baseline"] = None
     print(json.dumps(out))

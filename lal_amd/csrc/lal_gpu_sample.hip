@@ -2244,6 +2244,117 @@ __global__ __launch_bounds__(256) void lm_head_dot4_kernel(const int8_t *xq, con
     }
 }
 
+// Int8 LM head on the matrix cores, for 9..64 batch rows per launch:
+// logits[b][v] = (sx[b]*sw[v]) * (float)dot(xq[b], w[v]) with exact int32
+// sums (v_mfma_i32_16x16x64_i8; integer products and sums are exact in any
+// order).  Operand layout (checked on the device): A = 16 batch rows x 64 k,
+// lane l holds row l%16, bytes [16*(l/16), +16); B = 64 k x 16 vocab rows,
+// lane l holds row l%16, the same bytes; C = 16 x 16, lane l holds vocab row
+// l%16, batch rows 4*(l/16)+i.  Each workgroup owns an equal contiguous range
+// of vocab rows and walks it in tiles of 64 (16 per wave), streaming w once
+// (three 256-byte passes of k in flight per wave) against the batch's
+// activations staged in LDS 256 k-bytes at a time.
+constexpr int LMM_WAVES = 4;
+constexpr int LMM_TILE_V = 16 * LMM_WAVES;
+constexpr int LMM_KC = 256;
+constexpr int LMM_MAXB = 64;
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+template <int MT>
+__global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_mfma_kernel(const int8_t *xq, const float *sx, int n,
+                                                                      const int8_t *w, const float *sw, int V,
+                                                                      float *logits, int ld, int b0, int nb)
+{
+    __shared__ __align__(16) int8_t xs[2][MT * 16 * LMM_KC];
+    constexpr int XCH = MT * 16 * (LMM_KC / 16);                  // 16-byte chunks per stage
+    constexpr int XPT = (XCH + 64 * LMM_WAVES - 1) / (64 * LMM_WAVES);
+    const int wv = wave_id(), lane = lane_id(), tid = threadIdx.x;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int npass = (n + LMM_KC - 1) / LMM_KC;
+    const int vlo = (int)(((long long)V * blockIdx.x) / gridDim.x);
+    const int vhi = (int)(((long long)V * (blockIdx.x + 1)) / gridDim.x);
+
+    // activations of pass p -> registers (this thread's chunks)
+    auto fetch_x = [&](v4i (&xr)[XPT], int p) {
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int c = tid + j * 64 * LMM_WAVES;
+            const int row = c / (LMM_KC / 16), col = (c % (LMM_KC / 16)) * 16;
+            const int k = p * LMM_KC + col;
+            v4i v = {0, 0, 0, 0};
+            if (c < XCH && row < nb && k < n) v = *reinterpret_cast<const v4i *>(xq + (size_t)(b0 + row) * n + k);
+            xr[j] = v;
+        }
+    };
+    auto stage_x = [&](const v4i (&xr)[XPT], int buf) {
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int c = tid + j * 64 * LMM_WAVES;
+            if (c < XCH) {
+                const int row = c / (LMM_KC / 16), col = (c % (LMM_KC / 16)) * 16;
+                *reinterpret_cast<v4i *>(&xs[buf][row * LMM_KC + col]) = xr[j];
+            }
+        }
+    };
+
+    for (int t0 = vlo; t0 < vhi; t0 += LMM_TILE_V) {
+        const int v = t0 + 16 * wv + r16;  // this lane's w row (B operand column)
+        const bool vok = v < vhi;
+        const int8_t *wrow = w + (size_t)(vok ? v : 0) * n;
+        auto fetch_w = [&](v4i (&f)[4], int p) {
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int k = p * LMM_KC + 64 * s4 + 16 * g;
+                f[s4] = (vok && k < n) ? __builtin_nontemporal_load(reinterpret_cast<const v4i *>(wrow + k))
+                                       : v4i{0, 0, 0, 0};
+            }
+        };
+        v4i acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+        v4i w0[4], w1[4], w2[4];
+        v4i xr[XPT];
+        fetch_x(xr, 0);
+        fetch_w(w0, 0);
+        fetch_w(w1, 1);
+        __syncthreads();  // the previous tile is done with both stage buffers
+        stage_x(xr, 0);
+        if (npass > 1) fetch_x(xr, 1);
+        for (int p = 0; p < npass; ++p) {
+            fetch_w(w2, p + 2);
+            __syncthreads();  // stage p is in; stage p+1's buffer is free
+            if (p + 1 < npass) {
+                stage_x(xr, (p + 1) & 1);
+                if (p + 2 < npass) fetch_x(xr, p + 2);
+            }
+            const int8_t *xb = xs[p & 1];
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const v4i a = *reinterpret_cast<const v4i *>(xb + (mt * 16 + r16) * LMM_KC + 64 * s4 + 16 * g);
+                    acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w0[s4], acc[mt], 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                w0[s4] = w1[s4];
+                w1[s4] = w2[s4];
+            }
+        }
+        if (vok) {
+            const float swv = sw[v];
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int bb = mt * 16 + 4 * g + i;
+                    if (bb < nb) logits[(size_t)(b0 + bb) * ld + v] = (sx[b0 + bb] * swv) * (float)acc[mt][i];
+                }
+        }
+    }
+}
+
 // Rows whose length is not a multiple of 16 bytes: one wave per vocab row,
 // byte loads, same exact int32 accumulation.
 __global__ __launch_bounds__(256) void lm_head_scalar_kernel(const int8_t *xq, const float *sx, int n,
@@ -2401,6 +2512,7 @@ struct lal_gpu_ctx {
     int device;
     int max_batch;
     int max_vocab;
+    int ncu;  // compute units
     // slice lists (see KArgs): max_batch x FLAT_MAX entries, metadata for up
     // to MAX_SLICES slices per row, one arrival counter per row (zeroed here,
     // reset by every row's finisher)
@@ -2468,6 +2580,12 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     c->device = device;
     c->max_batch = max_batch;
     c->max_vocab = max_vocab;
+    {
+        int ncu = 0;
+        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, device) != hipSuccess || ncu <= 0)
+            ncu = 256;
+        c->ncu = ncu;
+    }
     const size_t nl = (size_t)max_batch * FLAT_MAX;
     hipError_t e = hipMalloc((void **)&c->lst_val, nl * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->lst_idx, nl * sizeof(int));
@@ -2497,8 +2615,8 @@ void lal_gpu_destroy(lal_gpu_ctx *ctx)
 
 // Slices per row.  A slice costs a fixed setup and finish on top of its
 // streaming, so rows are split only to give a small batch enough workgroups
-// (about one per slot: 4 per CU): slices of at least 64 Ki elements, or
-// 16 Ki for a batch of at most 4 rows (latency); list capacity above k.
+// (about one per slot: 4 per CU): slices of at least 64 Ki elements, 32 Ki
+// for at most 128 rows, 16 Ki for at most 16 rows; list capacity above k.
 constexpr int TARGET_WGS = 1024;
 static int choose_slices(int batch, int vocab, int k_eff, int flat)
 {
@@ -2506,7 +2624,7 @@ static int choose_slices(int batch, int vocab, int k_eff, int flat)
         const int n = atoi(env);
         if (n >= 1) return std::min(std::min(n, MAX_SLICES), std::max(1, flat / (k_eff + 1)));
     }
-    const int min_len = (batch <= 4) ? 16384 : 65536;
+    const int min_len = (batch <= 16) ? 16384 : (batch <= 128) ? 32768 : 65536;
     int n = (TARGET_WGS + batch - 1) / batch;
     n = std::min(n, std::max(1, vocab / min_len));
     n = std::min(n, std::max(1, flat / (k_eff + 1)));
@@ -2635,6 +2753,23 @@ int lal_gpu_lm_head_q8(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx, 
         hipLaunchKernelGGL(lm_head_scalar_kernel, dim3((vocab + 3) / 4), dim3(256), 0, s, d_xq, d_sx,
                            n, d_w, d_sw, vocab, d_logits, ld, batch);
         LAL_HIP(hipGetLastError());
+        return LAL_GPU_OK;
+    }
+    if (batch > LMH_MAXB) {
+        int per_cu = 4;
+        if (const char *env = getenv("LAL_GPU_LMH_WG")) per_cu = std::max(1, atoi(env));
+        const unsigned nwg = (unsigned)std::min(per_cu * ctx->ncu, (vocab + LMM_TILE_V - 1) / LMM_TILE_V);
+        for (int b0 = 0; b0 < batch; b0 += LMM_MAXB) {
+            const int nb = std::min(LMM_MAXB, batch - b0);
+            const dim3 g2(nwg), blk(64 * LMM_WAVES);
+            switch ((nb + 15) / 16) {
+            case 1: hipLaunchKernelGGL(lm_head_mfma_kernel<1>, g2, blk, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0, nb); break;
+            case 2: hipLaunchKernelGGL(lm_head_mfma_kernel<2>, g2, blk, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0, nb); break;
+            case 3: hipLaunchKernelGGL(lm_head_mfma_kernel<3>, g2, blk, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0, nb); break;
+            default: hipLaunchKernelGGL(lm_head_mfma_kernel<4>, g2, blk, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0, nb); break;
+            }
+            LAL_HIP(hipGetLastError());
+        }
         return LAL_GPU_OK;
     }
     const int waves = (vocab + LMH_ROWS - 1) / LMH_ROWS;

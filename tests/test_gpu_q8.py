@@ -122,3 +122,22 @@ def test_lm_head_qwen7b_shape(dev, orc, B):
     log(f"lm_head B={B}: {len(rows)} vocab rows x {B} bit-exact")
     for bb in (dW, dsw, dq, ds, dl):
         bb.close()
+
+
+@pytest.mark.parametrize("B", [9, 16, 33, 64, 100])
+def test_lm_head_matrix_core_path(dev, orc, B):
+    """Batches above 8 rows run on the int8 matrix cores in blocks of 64 rows:
+    every logit bit-exact (V = 5003 is not a multiple of the 64-row tiles,
+    n = 3584 - 64*3 leaves a partial 256-byte k pass)."""
+    from lal_amd import abi
+    V, n = 5003, 3392
+    rng = np.random.default_rng(B)
+    W = rng.integers(-127, 128, (V, n)).astype(np.int8)
+    sw = (rng.random(V) * 0.019 + 0.001).astype(np.float32)
+    x = synth.normal(70 + B, 0, B * n).reshape(B, n).astype(np.float32)
+    s, q = quantize(dev, x, 0)
+    out = lm_head(dev, q, s, W, sw)
+    for b in range(B):
+        want = orc.lm_head(q[b].copy(), s[b], W, sw)
+        assert np.array_equal(out[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
+    log(f"matrix-core lm_head B={B}: {B} x {V} bit-exact")
