@@ -16,6 +16,9 @@
  *                          compiler/lal.py:2218-2242 lal_filter_topk bans
  *                          (ban_last / ban_repeat(n) / ban_token(id)) on the
  *                          top-k pool, batched over rows
+ *   lal_gpu_sample_finish  tools/server/qwen7b_server.c:268-294, the softmax and
+ *                          draw after a lal_filter_topk plugin (keep-mask
+ *                          adapter for loaded .lal filters)
  *   lal_gpu_quantize_x     runtime/lal_q8_kernel.h:375-442 lal_quantize_x_int8
  *   lal_gpu_lm_head_q8     runtime/lal_q8_kernel.h:463-543
  *                          lal_lm_head_int8_range[_abs], caller
@@ -34,7 +37,7 @@
 extern "C" {
 #endif
 
-#define LAL_GPU_ABI_VERSION 1
+#define LAL_GPU_ABI_VERSION 2
 
 /* Limits.  top_k is capped at 512, the largest heap the reference samplers
  * hold (tools/server/qwen7b_server.c:239); beyond it the reference is
@@ -109,7 +112,33 @@ typedef struct lal_gpu_sample_io {
     uint8_t        *cand_kept;     /* [batch][cand_ld] 1 if in the final set */
     float          *out_history_vals; /* [batch][history_ld] logits[t] after the
                                          penalty for each history position */
+    float          *cand_vals;     /* [batch][cand_ld] processed logit of each pool id */
 } lal_gpu_sample_io;
+
+/* Finish over a pool filtered on the host: the keep-mask half of
+ * tools/server/qwen7b_server.c:257-294.  lal_gpu_sample (greedy off, no ban
+ * operations, cand_ld >= the pool size) yields the pool: out_n_cand,
+ * cand_ids (ascending) and cand_vals.  A lal_filter_topk plugin
+ * (compiler/lal.py:2205-2208) then clears entries of a keep mask; keep[i] = 1
+ * for pool entry i it left set, 0 for one it cleared.  Ids the plugin set
+ * outside the pool may follow the pool entries (any order, *n_cand counting
+ * them, cand_vals their processed logits) with keep = 2: like the reference
+ * they count as "something kept" and for the argmax, not for the softmax.
+ * This call restores the whole pool when nothing is kept, takes the softmax
+ * over the kept pool entries in id order and draws with the row's uniform
+ * (variant FILTERED: first id of the largest kept value, without a draw, when
+ * the sum is <= 0).  A row whose entries exceed cand_ld gets token -1. */
+typedef struct lal_gpu_finish_io {
+    const int      *n_cand;      /* [batch] */
+    int             cand_ld;
+    const int      *cand_ids;    /* [batch][cand_ld] */
+    const float    *cand_vals;   /* [batch][cand_ld] */
+    const uint8_t  *keep;        /* [batch][cand_ld] 0, 1 or 2 (see above) */
+    const float    *uniforms;    /* [batch] */
+    int            *out_token;   /* [batch] */
+    int            *out_n_kept;  /* [batch] or NULL */
+    float          *out_sum;     /* [batch] or NULL */
+} lal_gpu_finish_io;
 
 /* Context: owns per-device scratch for up to max_batch rows (candidate lists
  * exchanged between the workgroups of one row, 64 KiB per row, and one counter
@@ -125,6 +154,10 @@ void lal_gpu_destroy(lal_gpu_ctx *ctx);
 int  lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab,
                     const lal_gpu_sample_params *params,
                     const lal_gpu_sample_io *io, void *stream);
+
+int  lal_gpu_sample_finish(lal_gpu_ctx *ctx, int batch, int vocab,
+                           const lal_gpu_sample_params *params,
+                           const lal_gpu_finish_io *io, void *stream);
 
 /* Int8 LM head front end (runtime/lal_q8_kernel.h).
  * lal_gpu_quantize_x: x[batch][n] fp32 -> xq[batch][n] int8, sx[batch];

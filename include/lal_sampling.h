@@ -17,6 +17,8 @@
  *                          top_p)             nucleus of tools/server/gpt2_server.c:2908-2955
  *   lal_sample_token_filtered(...)            tools/server/qwen7b_server.c:219-295,
  *                                             only with LAL_SAMPLING_FILTERED defined
+ *   lal_sampling_set_filter_plugin(fn, dec)   qwen7b_server.c:160-215, 257-270: a
+ *                                             loaded lal_filter_topk plugin
  *
  * Behaviour kept from the reference:
  *   - logits is modified in place by the repetition penalty, once per
@@ -69,6 +71,12 @@ static void lal_recent_push(LalRecentTokens *rt, int tok)
 }
 
 /* ---- device state shared by the entry points below -------------------- */
+/* The plugin ABI of compiler/lal.py:2205-2208 (loaded .lal filters). */
+typedef int (*lal_token_decode_fn)(int token_id, char *out_buf, int max_len);
+typedef int (*lal_filter_topk_fn)(int *keep_mask, int n_vocab, int last_token,
+                                  const int *recent_tokens, int n_recent,
+                                  lal_token_decode_fn decode_fn);
+
 typedef struct {
     lal_gpu_ctx *ctx;
     void *stream;
@@ -77,6 +85,15 @@ typedef struct {
     int *d_hist, *d_tok, *d_ban;
     float *d_u, *d_sum, *d_hvals;
     int ban_last, ban_repeat, n_ban;
+    /* keep-mask adapter for a loaded lal_filter_topk plugin */
+    lal_filter_topk_fn plugin;
+    lal_token_decode_fn decode;
+    int *d_cids, *d_ncand;
+    float *d_cvals;
+    unsigned char *d_keep;
+    int *h_mask, *h_cids;
+    float *h_xvals;
+    unsigned char *h_keep;
 } lal_sampling_gpu_state;
 
 static lal_sampling_gpu_state lal__gs;
@@ -106,6 +123,17 @@ static void lal__release(void)
     lal_gpu_free(g->d_u);
     lal_gpu_free(g->d_sum);
     lal_gpu_free(g->d_hvals);
+    lal_gpu_free(g->d_cids);
+    lal_gpu_free(g->d_ncand);
+    lal_gpu_free(g->d_cvals);
+    lal_gpu_free(g->d_keep);
+    free(g->h_mask);
+    free(g->h_cids);
+    free(g->h_keep);
+    free(g->h_xvals);
+    g->h_mask = g->h_cids = NULL;
+    g->h_keep = NULL;
+    g->h_xvals = NULL;
     lal_gpu_destroy(g->ctx);
     g->ctx = NULL;
 }
@@ -133,6 +161,17 @@ static void lal__ensure(int vocab)
     LAL__CHECK(lal_gpu_malloc((void **)&g->d_sum, sizeof(float)), "lal_gpu_malloc");
     LAL__CHECK(lal_gpu_malloc((void **)&g->d_hvals, LAL_GPU_MAX_HISTORY * sizeof(float)),
                "lal_gpu_malloc");
+    /* the pool can be the whole row (ties), so the adapter's buffers hold V */
+    LAL__CHECK(lal_gpu_malloc((void **)&g->d_cids, (size_t)vocab * sizeof(int)), "lal_gpu_malloc");
+    LAL__CHECK(lal_gpu_malloc((void **)&g->d_ncand, sizeof(int)), "lal_gpu_malloc");
+    LAL__CHECK(lal_gpu_malloc((void **)&g->d_cvals, (size_t)vocab * sizeof(float)), "lal_gpu_malloc");
+    LAL__CHECK(lal_gpu_malloc((void **)&g->d_keep, (size_t)vocab), "lal_gpu_malloc");
+    g->h_mask = (int *)malloc((size_t)vocab * sizeof(int));
+    g->h_cids = (int *)malloc((size_t)vocab * sizeof(int));
+    g->h_keep = (unsigned char *)malloc((size_t)vocab);
+    g->h_xvals = (float *)malloc((size_t)vocab * sizeof(float));
+    if (!g->h_mask || !g->h_cids || !g->h_keep || !g->h_xvals)
+        lal__die("host allocation", LAL_GPU_E_NOMEM);
 }
 
 /* One row through lal_gpu_sample.  Uploads the row and history, runs the
@@ -193,6 +232,111 @@ static int lal__prepare(int vocab, int top_k, const int *recent, int *n_recent)
 
 static float lal__uniform(void) { return (float)rand() / (float)RAND_MAX; }
 
+/* Filtered sampler with a loaded lal_filter_topk plugin
+ * (tools/server/qwen7b_server.c:257-294): the GPU selects the pool, the host
+ * builds the keep mask over the whole vocabulary as the server does and calls
+ * the plugin, the GPU finishes (softmax over the kept pool entries, draw).
+ * Plugins from compiler/lal.py only clear entries; ids a plugin sets outside
+ * the pool go to the finish call as keep = 2 entries with their penalised
+ * logits, since the reference lets them block the restore of an emptied pool
+ * and win its sum <= 0 argmax. */
+static int lal__run_plugin(const float *logits, int vocab, lal_gpu_sample_params *p,
+                           const int *recent, int n_recent, float *hvals)
+{
+    lal_sampling_gpu_state *g = &lal__gs;
+    lal_gpu_sample_io io;
+    memset(&io, 0, sizeof io);
+    p->ban_last = p->ban_repeat = p->n_ban_ids = 0;
+    p->ban_ids = NULL;
+    LAL__CHECK(lal_gpu_memcpy_h2d(g->d_row, logits, (size_t)vocab * sizeof(float), g->stream),
+               "upload logits");
+    if (n_recent > 0) {
+        LAL__CHECK(lal_gpu_memcpy_h2d(g->d_hist, recent, (size_t)n_recent * sizeof(int), g->stream),
+                   "upload history");
+        io.history = g->d_hist;
+        io.history_ld = n_recent;
+        io.out_history_vals = g->d_hvals;
+    }
+    const float zero = 0.0f;
+    LAL__CHECK(lal_gpu_memcpy_h2d(g->d_u, &zero, sizeof zero, g->stream), "upload uniform");
+    io.logits = g->d_row;
+    io.ld = vocab;
+    io.uniforms = g->d_u;
+    io.out_token = g->d_tok;
+    io.out_n_cand = g->d_ncand;
+    io.cand_ld = vocab;
+    io.cand_ids = g->d_cids;
+    io.cand_vals = g->d_cvals;
+    LAL__CHECK(lal_gpu_sample(g->ctx, 1, vocab, p, &io, g->stream), "lal_gpu_sample");
+    int nc = 0;
+    LAL__CHECK(lal_gpu_memcpy_d2h(&nc, g->d_ncand, sizeof nc, g->stream), "download pool size");
+    if (n_recent > 0)
+        LAL__CHECK(lal_gpu_memcpy_d2h(hvals, g->d_hvals, (size_t)n_recent * sizeof(float), g->stream),
+                   "download history values");
+    LAL__CHECK(lal_gpu_stream_sync(g->stream), "stream sync");
+    if (nc < 1 || nc > vocab) lal__die("pool size", LAL_GPU_E_RANGE);
+    LAL__CHECK(lal_gpu_memcpy_d2h(g->h_cids, g->d_cids, (size_t)nc * sizeof(int), g->stream),
+               "download pool ids");
+    LAL__CHECK(lal_gpu_stream_sync(g->stream), "stream sync");
+    /* keep_mask[v] = (v in the pool), then the plugin */
+    memset(g->h_mask, 0, (size_t)vocab * sizeof(int));
+    for (int i = 0; i < nc; i++) g->h_mask[g->h_cids[i]] = 1;
+    const int last = (n_recent > 0) ? recent[n_recent - 1] : -1;
+    (void)g->plugin(g->h_mask, vocab, last, recent, n_recent, g->decode);
+    for (int i = 0; i < nc; i++) {
+        int *m = &g->h_mask[g->h_cids[i]];
+        g->h_keep[i] = *m ? 1 : 0;
+        *m = 0;
+    }
+    int nt = nc;  /* what is still set lies outside the pool */
+    for (int v = 0; v < vocab; v++) {
+        if (!g->h_mask[v]) continue;
+        float x = logits[v];
+        for (int j = 0; j < n_recent; j++)
+            if (recent[j] == v) x = hvals[j];
+        g->h_cids[nt] = v;
+        g->h_xvals[nt - nc] = x;
+        g->h_keep[nt] = 2;
+        nt++;
+    }
+    LAL__CHECK(lal_gpu_memcpy_h2d(g->d_keep, g->h_keep, (size_t)nt, g->stream), "upload keep flags");
+    if (nt > nc) {
+        const size_t ne = (size_t)(nt - nc);
+        LAL__CHECK(lal_gpu_memcpy_h2d(g->d_cids + nc, g->h_cids + nc, ne * sizeof(int), g->stream),
+                   "upload extra ids");
+        LAL__CHECK(lal_gpu_memcpy_h2d(g->d_cvals + nc, g->h_xvals, ne * sizeof(float), g->stream),
+                   "upload extra values");
+        LAL__CHECK(lal_gpu_memcpy_h2d(g->d_ncand, &nt, sizeof nt, g->stream), "upload entry count");
+    }
+    lal_gpu_finish_io fio;
+    memset(&fio, 0, sizeof fio);
+    fio.n_cand = g->d_ncand;
+    fio.cand_ld = vocab;
+    fio.cand_ids = g->d_cids;
+    fio.cand_vals = g->d_cvals;
+    fio.keep = g->d_keep;
+    fio.uniforms = g->d_u;
+    fio.out_token = g->d_tok;
+    fio.out_sum = g->d_sum;
+    /* as in lal__sample_common: u = 0 first, one rand() only if the sum is > 0 */
+    int tok = 0;
+    float sum = 0.0f;
+    LAL__CHECK(lal_gpu_sample_finish(g->ctx, 1, vocab, p, &fio, g->stream), "lal_gpu_sample_finish");
+    LAL__CHECK(lal_gpu_memcpy_d2h(&tok, g->d_tok, sizeof tok, g->stream), "download token");
+    LAL__CHECK(lal_gpu_memcpy_d2h(&sum, g->d_sum, sizeof sum, g->stream), "download sum");
+    LAL__CHECK(lal_gpu_stream_sync(g->stream), "stream sync");
+    if (sum > 0.0f) {
+        const float u = lal__uniform();
+        if (u != 0.0f) {
+            LAL__CHECK(lal_gpu_memcpy_h2d(g->d_u, &u, sizeof u, g->stream), "upload uniform");
+            LAL__CHECK(lal_gpu_sample_finish(g->ctx, 1, vocab, p, &fio, g->stream), "lal_gpu_sample_finish");
+            LAL__CHECK(lal_gpu_memcpy_d2h(&tok, g->d_tok, sizeof tok, g->stream), "download token");
+            LAL__CHECK(lal_gpu_stream_sync(g->stream), "stream sync");
+        }
+    }
+    return tok;
+}
+
 static int lal__sample_common(float *logits, int vocab_size, float temperature, int top_k,
                               float top_p, float rep_penalty, const int *recent, int n_recent,
                               int variant)
@@ -220,6 +364,8 @@ static int lal__sample_common(float *logits, int vocab_size, float temperature, 
         tok = lal__run(logits, vocab_size, &p, recent, n_recent, 0.0f, &sum, hv);
     } else if (variant != LAL_GPU_VARIANT_FILTERED) {
         tok = lal__run(logits, vocab_size, &p, recent, n_recent, lal__uniform(), &sum, hv);
+    } else if (lal__gs.plugin) {
+        tok = lal__run_plugin(logits, vocab_size, &p, recent, n_recent, hv);
     } else {
         /* The filtered sampler draws only when its softmax sum is positive.
          * Run with u = 0 first: when sum <= 0 that token (the argmax of the
@@ -271,6 +417,15 @@ static void lal_sampling_set_filter_ops(int ban_last, int ban_repeat, const int 
                    "upload ban ids");
         LAL__CHECK(lal_gpu_stream_sync(g->stream), "stream sync");
     }
+}
+
+/* Route lal_sample_token_filtered through a loaded lal_filter_topk plugin
+ * (the keep-mask adapter); NULL goes back to the operations set by
+ * lal_sampling_set_filter_ops.  decode_fn is passed to the plugin. */
+static void lal_sampling_set_filter_plugin(lal_filter_topk_fn fn, lal_token_decode_fn decode_fn)
+{
+    lal__gs.plugin = fn;
+    lal__gs.decode = decode_fn;
 }
 
 #ifdef LAL_SAMPLING_FILTERED

@@ -44,7 +44,14 @@ class SampleIO(C.Structure):
                 ("out_threshold", C.c_void_p), ("out_n_cand", C.c_void_p),
                 ("out_n_kept", C.c_void_p), ("out_sum", C.c_void_p),
                 ("cand_ld", C.c_int), ("cand_ids", C.c_void_p), ("cand_probs", C.c_void_p),
-                ("cand_kept", C.c_void_p), ("out_history_vals", C.c_void_p)]
+                ("cand_kept", C.c_void_p), ("out_history_vals", C.c_void_p),
+                ("cand_vals", C.c_void_p)]
+
+
+class FinishIO(C.Structure):
+    _fields_ = [("n_cand", C.c_void_p), ("cand_ld", C.c_int), ("cand_ids", C.c_void_p),
+                ("cand_vals", C.c_void_p), ("keep", C.c_void_p), ("uniforms", C.c_void_p),
+                ("out_token", C.c_void_p), ("out_n_kept", C.c_void_p), ("out_sum", C.c_void_p)]
 
 
 # (name, restype, argtypes) for every exported entry point
@@ -58,6 +65,7 @@ EXPORTS = [
     ("lal_gpu_create", _i, [C.POINTER(_vp), _i, _i, _i]),
     ("lal_gpu_destroy", None, [_vp]),
     ("lal_gpu_sample", _i, [_vp, _i, _i, C.POINTER(SampleParams), C.POINTER(SampleIO), _vp]),
+    ("lal_gpu_sample_finish", _i, [_vp, _i, _i, C.POINTER(SampleParams), C.POINTER(FinishIO), _vp]),
     ("lal_gpu_quantize_x", _i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     ("lal_gpu_lm_head_q8", _i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
     ("lal_gpu_uniforms_rand", None, [_u, _i, C.POINTER(_f), _i]),
@@ -188,6 +196,10 @@ class Device:
     def sample(self, batch, vocab, params, io):
         check(self.lib.lal_gpu_sample(self.ctx, batch, vocab, C.byref(params), C.byref(io),
                                       self.stream), "sample")
+
+    def finish(self, batch, vocab, params, fio):
+        check(self.lib.lal_gpu_sample_finish(self.ctx, batch, vocab, C.byref(params),
+                                             C.byref(fio), self.stream), "sample_finish")
 
     def event(self):
         e = C.c_void_p()

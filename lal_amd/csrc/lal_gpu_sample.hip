@@ -274,6 +274,7 @@ struct KArgs {
     int *cand_ids;
     float *cand_probs;
     uint8_t *cand_kept;
+    float *cand_vals;
     float *out_hvals;
     const int *ban_ids;
     int n_ban;
@@ -1076,6 +1077,7 @@ __device__ __forceinline__ void rescan_write_cands(const KArgs &A, SM &S, const 
                                          : in_nucleus(A, S, N, y_of[q], e) && !(use_ban && is_banned(S, e));
                 const size_t o = (size_t)b * A.cand_ld + pos;
                 if (A.cand_ids) A.cand_ids[o] = e;
+                if (A.cand_vals) A.cand_vals[o] = y_of[q];
                 if (A.cand_kept) A.cand_kept[o] = kept ? 1 : 0;
                 if (A.cand_probs)
                     A.cand_probs[o] = greedy ? (kept ? 1.0f : 0.0f)
@@ -1357,6 +1359,7 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
     if (valid && lane < A.cand_ld) {
         const size_t o = (size_t)b * A.cand_ld + lane;
         if (A.cand_ids) A.cand_ids[o] = id;
+        if (A.cand_vals) A.cand_vals[o] = y;
         if (A.cand_kept) A.cand_kept[o] = kept ? 1 : 0;
         if (A.cand_probs) A.cand_probs[o] = kept ? e2 / sum : 0.0f;
     }
@@ -1487,6 +1490,7 @@ __device__ __forceinline__ RowResult block_epilogue(const KArgs &A, SM &S, int n
             if (j < nc && j < A.cand_ld) {
                 const size_t o = (size_t)b * A.cand_ld + j;
                 if (A.cand_ids) A.cand_ids[o] = S.cidx[j];
+                if (A.cand_vals) A.cand_vals[o] = S.cval[j];
                 if (A.cand_kept) A.cand_kept[o] = kept[r] ? 1 : 0;
                 if (A.cand_probs) A.cand_probs[o] = kept[r] ? e2[r] / res.sum : 0.0f;
             }
@@ -2044,6 +2048,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             for (int j = tid; j < nc && j < A.cand_ld; j += WG) {
                 const size_t o = (size_t)b * A.cand_ld + j;
                 if (A.cand_ids) A.cand_ids[o] = S.cidx[j];
+                if (A.cand_vals) A.cand_vals[o] = S.cval[j];
                 if (A.cand_kept) A.cand_kept[o] = (j == 0);
                 if (A.cand_probs) A.cand_probs[o] = (j == 0) ? 1.0f : 0.0f;
             }
@@ -2140,6 +2145,129 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
                 if (key >= 0 && (S.hinfo[s] & HCOUNT_MASK)) A.logits_w[(size_t)b * A.ld + key] = pv[s];
             }
         }
+    }
+}
+
+// ---------------------------------------------------------------------------
+// Finish over a host-filtered pool (tools/server/qwen7b_server.c:268-294,
+// after the lal_filter_topk plugin has cleared entries of the keep mask): the
+// pool ids ascending with their processed logits, a keep flag per entry; the
+// pool is restored when no entry is kept; softmax over the kept entries in id
+// order, argmax without a draw when the sum is <= 0 (filtered variant), else
+// the first kept id whose running sum reaches u*sum.
+// ---------------------------------------------------------------------------
+struct FinishArgs {
+    int V, variant;
+    unsigned flags;
+    float T;
+    int cand_ld;
+    const int *n_cand;
+    const int *ids;
+    const float *vals;
+    const uint8_t *keep;
+    const float *uniforms;
+    int *out_token, *out_n_kept;
+    float *out_sum;
+};
+
+struct FSmem {
+    float ep[RS_CHUNK];
+    float redf[NWAVE];
+    int redi[NWAVE];
+    int redi2[NWAVE];
+    int wsum[2][NWAVE];
+    uint64_t exptab[32];
+};
+
+__global__ __launch_bounds__(WG) void finish_rows_kernel(FinishArgs F)
+{
+    __shared__ FSmem S;
+    const int b = blockIdx.x, tid = threadIdx.x;
+    if (tid < 32) S.exptab[tid] = kExp2Tab[tid];
+    const int n = F.n_cand[b];
+    const size_t o = (size_t)b * F.cand_ld;
+    if (n < 0 || n > F.cand_ld) {  // pool not captured in full
+        if (tid == 0) {
+            F.out_token[b] = -1;
+            if (F.out_n_kept) F.out_n_kept[b] = -1;
+        }
+        return;
+    }
+    // keep: 0 dropped, 1 kept pool entry, 2 kept entry outside the pool (it
+    // counts for "anything kept" and for the sum <= 0 argmax, not the softmax)
+    int nk = 0, na = 0;
+    float mk = -INFINITY, ma = -INFINITY;
+    for (int i = tid; i < n; i += WG) {
+        const uint8_t k = F.keep[o + i];
+        const float x = F.vals[o + i];
+        nk += (k == 1) ? 1 : 0;
+        na += k ? 1 : 0;
+        if (k == 1) mk = fmaxf(mk, x);
+        if (k) ma = fmaxf(ma, x);
+    }
+    nk = block_sum(S, nk);
+    na = block_sum(S, na);
+    const bool restore = (na == 0);  // nothing kept: the whole pool
+    if (restore) {
+        mk = -INFINITY;
+        for (int i = tid; i < n; i += WG) mk = fmaxf(mk, F.vals[o + i]);
+    }
+    const float kmax = block_max(S, mk);
+    const float amax = restore ? kmax : block_max(S, ma);
+    const float mx = (kmax > -1e30f) ? kmax : -1e30f;
+    // sequential sum in id order, RS_CHUNK entries at a time
+    float acc = 0.0f;
+    for (int c0 = 0; c0 < n; c0 += RS_CHUNK) {
+        const int m = min(RS_CHUNK, n - c0);
+        __syncthreads();
+        for (int i = tid; i < m; i += WG) {
+            const bool kp = restore || F.keep[o + c0 + i] == 1;
+            S.ep[i] = kp ? glibc_expf((F.vals[o + c0 + i] - mx) / F.T, S.exptab) : -1.0f;
+        }
+        acc = block_seq_prefix(S, S.ep, m, acc);
+    }
+    const float sum = acc;
+    int token = F.V - 1;
+    if (F.variant == LAL_GPU_VARIANT_FILTERED && sum <= 0.0f) {
+        // first id of the largest kept value above -1e30 (ids of entries
+        // outside the pool need not be in order)
+        int first = INT_MAX;
+        for (int i = tid; i < n; i += WG)
+            if ((restore || F.keep[o + i]) && F.vals[o + i] == amax && amax > -1e30f)
+                first = min(first, F.ids[o + i]);
+        first = block_min(S, first);
+        token = (first == INT_MAX) ? 0 : first;
+    } else {
+        const float r = (F.uniforms ? F.uniforms[b] : 0.0f) * sum;
+        if ((F.flags & LAL_GPU_F_DRAW_GPT2) && r == 0.0f) {
+            token = 0;
+        } else {
+            float run = 0.0f;
+            for (int c0 = 0; c0 < n; c0 += RS_CHUNK) {
+                const int m = min(RS_CHUNK, n - c0);
+                __syncthreads();
+                for (int i = tid; i < m; i += WG) {
+                    const bool kp = restore || F.keep[o + c0 + i] == 1;
+                    S.ep[i] = kp ? glibc_expf((F.vals[o + c0 + i] - mx) / F.T, S.exptab) : -1.0f;
+                }
+                run = block_seq_prefix(S, S.ep, m, run);
+                int first = INT_MAX;
+                for (int i = tid; i < m; i += WG) {
+                    const bool kp = restore || F.keep[o + c0 + i] == 1;
+                    if (kp && r <= S.ep[i]) first = min(first, i);
+                }
+                first = block_min(S, first);
+                if (first != INT_MAX) {
+                    token = F.ids[o + c0 + first];
+                    break;
+                }
+            }
+        }
+    }
+    if (tid == 0) {
+        F.out_token[b] = token;
+        if (F.out_n_kept) F.out_n_kept[b] = restore ? n : nk;
+        if (F.out_sum) F.out_sum[b] = sum;
     }
 }
 
@@ -2648,7 +2776,8 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     if (p->n_ban_ids > 0 && !p->ban_ids) return LAL_GPU_E_INVAL;
     if (p->variant != LAL_GPU_VARIANT_BASIC && p->variant != LAL_GPU_VARIANT_FILTERED)
         return LAL_GPU_E_INVAL;
-    if (io->cand_ld < 0 || (io->cand_ld > 0 && !io->cand_ids && !io->cand_probs && !io->cand_kept))
+    if (io->cand_ld < 0 ||
+        (io->cand_ld > 0 && !io->cand_ids && !io->cand_probs && !io->cand_kept && !io->cand_vals))
         return LAL_GPU_E_INVAL;
     if (io->out_history_vals && !io->history) return LAL_GPU_E_INVAL;
 
@@ -2674,6 +2803,7 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     A.cand_ids = io->cand_ids;
     A.cand_probs = io->cand_probs;
     A.cand_kept = io->cand_kept;
+    A.cand_vals = io->cand_vals;
     A.out_hvals = io->out_history_vals;
     A.ban_ids = p->ban_ids;
     A.n_ban = p->n_ban_ids;
@@ -2726,6 +2856,34 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     else if (A.allow) LAL_LAUNCH(false, true);
     else LAL_LAUNCH(false, false);
 #undef LAL_LAUNCH
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_sample_finish(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_params *p,
+                          const lal_gpu_finish_io *io, void *stream)
+{
+    if (!ctx || !p || !io || batch <= 0 || vocab <= 0) return LAL_GPU_E_INVAL;
+    if (batch > ctx->max_batch) return LAL_GPU_E_RANGE;
+    if (!io->n_cand || !io->cand_ids || !io->cand_vals || !io->keep || !io->out_token || io->cand_ld <= 0)
+        return LAL_GPU_E_INVAL;
+    if (p->variant != LAL_GPU_VARIANT_BASIC && p->variant != LAL_GPU_VARIANT_FILTERED) return LAL_GPU_E_INVAL;
+    if (!(p->temperature > 0.0f)) return LAL_GPU_E_INVAL;  // greedy rows have no softmax to finish
+    FinishArgs F;
+    F.V = vocab;
+    F.variant = p->variant;
+    F.flags = p->flags;
+    F.T = p->temperature;
+    F.cand_ld = io->cand_ld;
+    F.n_cand = io->n_cand;
+    F.ids = io->cand_ids;
+    F.vals = io->cand_vals;
+    F.keep = io->keep;
+    F.uniforms = io->uniforms;
+    F.out_token = io->out_token;
+    F.out_n_kept = io->out_n_kept;
+    F.out_sum = io->out_sum;
+    hipLaunchKernelGGL(finish_rows_kernel, dim3(batch), dim3(WG), 0, (hipStream_t)stream, F);
     LAL_HIP(hipGetLastError());
     return LAL_GPU_OK;
 }

@@ -32,6 +32,9 @@ class DropIn:
         L.dh_set_filter_ops.argtypes = [C.c_int, C.c_int, _ip, C.c_int]
         L.dh_recent_push.argtypes = [_ip, _ip, C.c_int]
         L.dh_globals.argtypes = [_ip, _ip, _fp]
+        L.dh_set_filter_plugin.argtypes = [C.c_void_p]
+        self.plugins = {nm: C.cast(getattr(L, f"dh_plugin_{nm}"), C.c_void_p).value
+                        for nm in ("clear_all", "thin3", "swap_out", "add_out")}
 
     def sample(self, row, T, k, pen, hist, filtered=False):
         """row: float32 array, modified in place like the reference."""
@@ -46,6 +49,10 @@ class DropIn:
     def set_filter_ops(self, ban_last=0, ban_repeat=0, ban_ids=None):
         ids = None if not ban_ids else np.ascontiguousarray(ban_ids, np.int32)
         self.L.dh_set_filter_ops(ban_last, ban_repeat, _ptr(ids, _ip), 0 if ids is None else len(ids))
+
+    def set_filter_plugin(self, fn):
+        """fn: address of a lal_filter_topk function, or None."""
+        self.L.dh_set_filter_plugin(fn)
 
     def srand(self, seed):
         self.L.dh_srand(seed)

@@ -63,11 +63,13 @@ class GpuRun:
             bufs["cids"] = dev.alloc(4 * B * cand_ld)
             bufs["cprobs"] = dev.alloc(4 * B * cand_ld)
             bufs["ckept"] = dev.alloc(B * cand_ld)
+            bufs["cvals"] = dev.alloc(4 * B * cand_ld)
             dev.lib.lal_gpu_memset(abi.ptr(bufs["cids"]), 0xFF, 4 * B * cand_ld, dev.stream)
             io.cand_ld = cand_ld
             io.cand_ids = bufs["cids"].ptr
             io.cand_probs = bufs["cprobs"].ptr
             io.cand_kept = bufs["ckept"].ptr
+            io.cand_vals = bufs["cvals"].ptr
         if want_hvals and hist is not None:
             bufs["hvals"] = dev.alloc(4 * hist.size)
             io.out_history_vals = bufs["hvals"].ptr
@@ -85,6 +87,7 @@ class GpuRun:
             res["cand_ids"] = bufs["cids"].download((B, cand_ld), np.int32)
             res["cand_probs"] = bufs["cprobs"].download((B, cand_ld), np.float32)
             res["cand_kept"] = bufs["ckept"].download((B, cand_ld), np.uint8)
+            res["cand_vals"] = bufs["cvals"].download((B, cand_ld), np.float32)
         if want_hvals and hist is not None:
             res["hvals"] = bufs["hvals"].download(hist.shape, np.float32)
         if flags & abi.F_WRITEBACK:
@@ -142,3 +145,34 @@ def assert_same(gpu, ora, cand_ld=0, check_probs=True, rows=None):
                     rel = np.abs(pg - po) / np.maximum(np.abs(po), 1e-30)
                 ok = (pg == po) | (np.isnan(pg) & np.isnan(po)) | (rel <= 1e-5)
                 assert np.all(ok), f"probs row {b}: max rel {np.nanmax(rel)}"
+
+
+def gpu_finish(dev, n_cand, cand_ids, cand_vals, keep, V, T=0.8, variant=1, flags=0, u=None):
+    """lal_gpu_sample_finish over host arrays ([B], [B][ld] ids/vals/keep)."""
+    n_cand = np.ascontiguousarray(n_cand, np.int32)
+    B = n_cand.shape[0]
+    ld = cand_ids.shape[1]
+    if u is None:
+        u = np.full(B, 0.5, np.float32)
+    bufs = {"n": dev.put(n_cand), "ids": dev.put(np.ascontiguousarray(cand_ids, np.int32)),
+            "vals": dev.put(np.ascontiguousarray(cand_vals, np.float32)),
+            "keep": dev.put(np.ascontiguousarray(keep, np.uint8)),
+            "u": dev.put(np.ascontiguousarray(u, np.float32)),
+            "tok": dev.alloc(4 * B), "nk": dev.alloc(4 * B), "sum": dev.alloc(4 * B)}
+    fio = abi.FinishIO()
+    fio.n_cand = bufs["n"].ptr
+    fio.cand_ld = ld
+    fio.cand_ids = bufs["ids"].ptr
+    fio.cand_vals = bufs["vals"].ptr
+    fio.keep = bufs["keep"].ptr
+    fio.uniforms = bufs["u"].ptr
+    fio.out_token = bufs["tok"].ptr
+    fio.out_n_kept = bufs["nk"].ptr
+    fio.out_sum = bufs["sum"].ptr
+    dev.finish(B, V, abi.make_params(temperature=T, variant=variant, flags=flags), fio)
+    dev.sync()
+    res = {"token": bufs["tok"].download(B, np.int32), "n_kept": bufs["nk"].download(B, np.int32),
+           "sum": bufs["sum"].download(B, np.float32)}
+    for b in bufs.values():
+        b.close()
+    return res

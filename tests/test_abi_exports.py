@@ -41,7 +41,7 @@ def test_struct_layouts_match_header():
     text = open(os.path.join(ROOT, "include/lal_gpu_sample.h")).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
     for cname, py in (("lal_gpu_sample_params", abi.SampleParams),
-                      ("lal_gpu_sample_io", abi.SampleIO)):
+                      ("lal_gpu_sample_io", abi.SampleIO), ("lal_gpu_finish_io", abi.FinishIO)):
         body = re.search(r"typedef struct " + cname + r"\s*\{(.*?)\}", text, re.S).group(1)
         names = re.findall(r"\**(\w+)\s*;", body)
         assert names == [f for f, _ in py._fields_], cname
@@ -57,7 +57,8 @@ def test_no_device_calls_without_gpu():
     want = golden_cases.load()["uniforms"]["42"]["u_bits"][:4]
     import numpy as np
     assert list(np.frombuffer(bytes(out), np.uint32)) == want
-    assert lib.lal_gpu_abi_version() == 1
+    hdr = open(os.path.join(ROOT, "include/lal_gpu_sample.h")).read()
+    assert lib.lal_gpu_abi_version() == int(re.search(r"LAL_GPU_ABI_VERSION (\d+)", hdr).group(1))
     assert lib.lal_gpu_strerror(-2) == b"size above a context or library limit"
 
 

@@ -13,6 +13,9 @@ cover directly.
   p <= 0 leave the top-k pool untouched; the final probabilities are the
   pool's renormalised over the kept set; u = 0 and u = 1 return the first and
   last kept ids; the gpt2 draw returns id 0 when r == 0.
+* Keep-mask plugins beyond the ban rules (clear all, thin, ids set outside the
+  pool) are checked against the reference's filtered sampler with the same
+  plugin loaded.
 """
 import numpy as np
 import pytest
@@ -87,6 +90,73 @@ def test_logit_ops_against_reference(ref, variant):
         assert np.array_equal(x.view(np.uint32), base.view(np.uint32)), f"case {i}: in-place row"
         cases += 1
     assert cases == 60
+
+
+def _py_plugins():
+    """lal_filter_topk plugins (compiler/lal.py:2205-2208 ABI) beyond the ban
+    rules: clear everything (restore), thin the pool, clear the pool and set
+    ids outside it (sum <= 0 argmax over those), set ids outside a kept pool."""
+    import ctypes as C
+    proto = C.CFUNCTYPE(C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.POINTER(C.c_int),
+                        C.c_int, C.c_void_p)
+
+    def view(km, n):
+        return np.ctypeslib.as_array(km, shape=(n,))
+
+    def clear_all(km, n, last, rec, nr, dec):
+        view(km, n)[:] = 0
+        return 0
+
+    def thin3(km, n, last, rec, nr, dec):
+        m = view(km, n)
+        on = np.nonzero(m)[0]
+        m[on[np.arange(len(on)) % 3 != 1]] = 0
+        return 0
+
+    def swap_out(km, n, last, rec, nr, dec):
+        m = view(km, n)
+        pool = np.nonzero(m)[0]
+        for i in range(nr):
+            if 0 <= rec[i] < n:
+                m[rec[i]] = 1
+        if n > 7:
+            m[7] = 1
+        m[pool] = 0
+        return 0
+
+    def add_out(km, n, last, rec, nr, dec):
+        view(km, n)[3::97] = 1
+        return 0
+
+    fns = {"clear_all": clear_all, "thin3": thin3, "swap_out": swap_out, "add_out": add_out}
+    return {k: proto(f) for k, f in fns.items()}
+
+
+def test_plugin_semantics_against_reference(ref):
+    """The oracle's keep-mask handling (restore only when nothing at all is
+    kept; ids set outside the pool count for that and for the sum <= 0 argmax,
+    not for the softmax) against qwen7b_server.c:257-294 compiled as is."""
+    import ctypes as C
+    plugins = _py_plugins()
+    cases = 0
+    for i in range(40):
+        V = [50, 333, 1000, 4099][i % 4]
+        kind = ["gauss", "zipf", "ties", "outliers", "neginf"][i % 5]
+        row = synth.make_row(kind, 1500 + i, V)
+        hist = synth.history(1600 + i, 1, 24, V, with_invalid=(i % 3 == 0))[0]
+        k = [1, 7, 40, 64][i % 4]
+        for name, cb in sorted(plugins.items()):
+            fp = C.cast(cb, C.c_void_p).value
+            seed = 2000 + 17 * i + len(name)
+            r_ref = row.copy()
+            tok_ref = ref.sample(r_ref, V, 0.9, k, 1.1, hist, seed, filtered=True, filt=fp)
+            x = row.copy()
+            p = make_params(temperature=0.9, top_k=k, rep_penalty=1.1, variant=VARIANT_FILTERED)
+            tok, *_ = ORC.sample_row(x, p, hist=hist, u=ORC.uniforms(seed, 1)[0], filt=fp)
+            assert tok == tok_ref, f"case {i} {name}: oracle {tok} reference {tok_ref}"
+            assert np.array_equal(x.view(np.uint32), r_ref.view(np.uint32))
+            cases += 1
+    assert cases == 160
 
 
 def _pool(row, k, T):
