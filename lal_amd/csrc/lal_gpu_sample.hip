@@ -251,6 +251,9 @@ struct Smem {
     int redi2[NWAVE];
     int sel_digit;
     int sel_rem;
+    int gcount;           // keys gathered by the select's final step
+    unsigned wkmax[NWAVE];  // per-wave range of the live buffer keys
+    unsigned wkmin[NWAVE];
     uint64_t exptab[32];  // glibc's 2^(i/32) table (LDS copy of kExp2Tab)
 };
 
@@ -296,6 +299,8 @@ struct KArgs {
     int *lst_idx;       // [batch][nslice][lcap] candidate ids
     int4 *lst_meta;     // [batch][nslice] (count, threshold bits, strict, -)
     unsigned *arrive;   // [batch] slices finished; reset by the finisher
+    int ncu;            // compute units: workgroups [3*ncu, 4*ncu) are the
+                        // fourth (youngest) resident on their CU
 };
 
 // block reductions (barriers inside; callers keep control flow uniform)
@@ -549,6 +554,52 @@ __device__ __forceinline__ uint32_t wave_kth_lane_key(uint32_t key, int k)
     return K;
 }
 
+// k-th largest of the keys q[0..NQ) held by the wave's lanes (key 0 = none):
+// the largest K with at least k keys >= K, 0 when fewer than k are nonzero.
+// The bits above the highest one where the largest and smallest nonzero keys
+// differ are common to every candidate; the rest are decided two at a time
+// (three independent ballot counts per step).  Wave-synchronous.
+template <int NQ>
+__device__ __forceinline__ int ballot_count_ge(const uint32_t (&q)[NQ], uint32_t c)
+{
+    int n = 0;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) n += __popcll(__ballot(q[i] >= c));
+    return n;
+}
+
+template <int NQ>
+__device__ __forceinline__ uint32_t wave_kth_keys(const uint32_t (&q)[NQ], int k)
+{
+    uint32_t mx = 0u, mn = 0xFFFFFFFFu;
+    int nz = 0;
+#pragma unroll
+    for (int i = 0; i < NQ; ++i) {
+        mx = max(mx, q[i]);
+        if (q[i]) mn = min(mn, q[i]);
+        nz += __popcll(__ballot(q[i] != 0u));
+    }
+    if (nz < k) return 0u;
+    mx = wave_max_u(mx);
+    mn = wave_min_u(mn);
+    if (mn >= mx) return mx;
+    int bit = 31 - __builtin_clz(mn ^ mx);  // highest differing bit
+    uint32_t K = (bit == 31) ? 0u : (mx & ~((2u << bit) - 1u));
+    if (!(bit & 1)) {  // odd number of bits left: one single step
+        const uint32_t c = K | (1u << bit);
+        if (ballot_count_ge<NQ>(q, c) >= k) K = c;
+        --bit;
+    }
+    for (; bit >= 1; bit -= 2) {
+        const uint32_t c1 = K | (1u << (bit - 1)), c2 = K | (2u << (bit - 1)),
+                       c3 = K | (3u << (bit - 1));
+        const int n1 = ballot_count_ge<NQ>(q, c1), n2 = ballot_count_ge<NQ>(q, c2),
+                  n3 = ballot_count_ge<NQ>(q, c3);
+        K = (n3 >= k) ? c3 : (n2 >= k) ? c2 : (n1 >= k) ? c1 : K;
+    }
+    return K;
+}
+
 // ---------------------------------------------------------------------------
 // Per-wave state and candidate buffer
 // ---------------------------------------------------------------------------
@@ -775,85 +826,181 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
     }
 }
 
+// Range of the live buffer keys over the block, from the per-wave ranges the
+// waves stored in S.wkmax / S.wkmin (0 / 0xFFFFFFFF for none).
+template <class SM>
+__device__ __forceinline__ void block_key_range(const SM &S, uint32_t &kmin, uint32_t &kmax)
+{
+    kmax = 0u;
+    kmin = 0xFFFFFFFFu;
+#pragma unroll
+    for (int ww = 0; ww < NWAVE; ++ww) {
+        kmax = max(kmax, (uint32_t)S.wkmax[ww]);
+        kmin = min(kmin, (uint32_t)S.wkmin[ww]);
+    }
+}
+
 // Block radix select over the union of the wave buffers (each thread reads
-// its own wave's entries).  Requires >= k entries in total.
+// its own wave's entries).  Requires >= k entries in total; kmin / kmax is the
+// range of the live keys (block_key_range).  The bits above the highest one
+// where kmin and kmax differ are common; the rest go 8 per pass with one
+// barrier each (three histograms in rotation, and every wave derives the
+// digit itself).  Once the chosen bin holds at most 64 keys they are gathered
+// and every wave ranks them directly.  Every thread calls it; no barrier is
+// needed after it before the wave buffers or S.wsum are written again.
 template <int CAPW, class SM>
-__device__ __forceinline__ uint32_t block_kth_union(SM &S, int k)
+__device__ __forceinline__ uint32_t block_kth_union(SM &S, int k, uint32_t kmin, uint32_t kmax)
 {
     constexpr int PK = CAPW / 64;  // entries per lane of its own wave's buffer
-    unsigned *hist = S.u.h.whist[0];
+    if (kmin >= kmax) return kmax;  // every live key is equal (k <= count)
     const int w = wave_id(), lane = lane_id();
     const int cnt = S.wcnt[w];
     const float *bv = S.cval + w * CAPW;
-    // keys of the live entries (0 = none), and their range over the block
+    // keys of the live entries (0 = none); reads stay inside the wave's buffer
     uint32_t key[PK];
-    uint32_t kmax = 0u, kmin = 0xFFFFFFFFu;
 #pragma unroll
     for (int r = 0; r < PK; ++r) {
         const int j = lane + 64 * r;
-        const float v = (j < cnt) ? bv[j] : NAN;
-        key[r] = (v == v) ? fkey(v) : 0u;
-        if (key[r]) {
-            kmax = max(kmax, key[r]);
-            kmin = min(kmin, key[r]);
-        }
+        const float v = bv[j];
+        key[r] = (j < cnt && v == v) ? fkey(v) : 0u;
     }
-    kmax = (uint32_t)wave_max_u(kmax);
-    kmin = (uint32_t)wave_min_u(kmin);
+    S.u.h.whist[0][threadIdx.x] = 0;
+    S.u.h.whist[1][threadIdx.x] = 0;
+    if (threadIdx.x == 0) S.gcount = 0;
     __syncthreads();
-    if (lane == 0) {
-        S.redi[w] = (int)kmax;
-        S.redi2[w] = (int)kmin;
-    }
-    __syncthreads();
-#pragma unroll
-    for (int ww = 0; ww < NWAVE; ++ww) {
-        kmax = max(kmax, (uint32_t)S.redi[ww]);
-        kmin = min(kmin, (uint32_t)S.redi2[ww]);
-    }
-    if (kmin >= kmax) {  // every live key is equal (k <= count)
-        __syncthreads();
-        return kmax;
-    }
-    // the bits above the first one where the keys differ are common: select
-    // from there, 8 bits per pass
     const int L = __builtin_clz(kmin ^ kmax);
     uint32_t pmask = L ? ~0u << (32 - L) : 0u;
     uint32_t prefix = kmax & pmask;
     int rem = k;
-    for (int hi = 31 - L; hi >= 0; hi -= 8) {
+    int p = 0;
+    for (int hi = 31 - L; hi >= 0; hi -= 8, ++p) {
+        unsigned *hist = S.u.h.whist[p % 3];
         const int lo = max(hi - 7, 0);
         const uint32_t dmask = (hi - lo == 31) ? ~0u : ((1u << (hi - lo + 1)) - 1u);
-        __syncthreads();
-        hist[threadIdx.x] = 0;
-        __syncthreads();
 #pragma unroll
         for (int r = 0; r < PK; ++r)
             if (key[r] && (key[r] & pmask) == prefix) atomicAdd(&hist[(key[r] >> lo) & dmask], 1u);
+        // the next pass's histogram was last read before the previous barrier
+        S.u.h.whist[(p + 1) % 3][threadIdx.x] = 0;
         __syncthreads();
-        if (w == 0) {
-            const int b0 = 255 - 4 * lane;
-            const int h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
-            const int lsum = h0 + h1 + h2 + h3;
-            const int incl = wave_incl_scan(lsum);
-            const int excl = incl - lsum;
-            if (excl < rem && rem <= incl) {
-                int r = rem - excl, d;
-                if (r <= h0) d = b0;
-                else if ((r -= h0) <= h1) d = b0 - 1;
-                else if ((r -= h1) <= h2) d = b0 - 2;
-                else { r -= h2; d = b0 - 3; }
-                S.sel_digit = d;
-                S.sel_rem = r;
-            }
-        }
-        __syncthreads();
-        prefix |= (uint32_t)S.sel_digit << lo;
+        const int b0 = 255 - 4 * lane;
+        const int h0 = hist[b0], h1 = hist[b0 - 1], h2 = hist[b0 - 2], h3 = hist[b0 - 3];
+        const int lsum = h0 + h1 + h2 + h3;
+        const int incl = wave_incl_scan(lsum);
+        const int excl = incl - lsum;
+        const bool hit = (excl < rem && rem <= incl);
+        int r = rem - excl, d = b0, hb = h0;
+        if (r <= h0) { d = b0; hb = h0; }
+        else if ((r -= h0) <= h1) { d = b0 - 1; hb = h1; }
+        else if ((r -= h1) <= h2) { d = b0 - 2; hb = h2; }
+        else { r -= h2; d = b0 - 3; hb = h3; }
+        const unsigned long long hm = __ballot(hit);
+        const int src = hm ? (int)__builtin_ctzll(hm) : 0;
+        d = readlane_i(d, src);
+        r = readlane_i(r, src);
+        hb = readlane_i(hb, src);
+        prefix |= (uint32_t)d << lo;
         pmask |= dmask << lo;
-        rem = S.sel_rem;
+        rem = r;
+        if (lo > 0 && hb <= 64) {
+            // few keys left with this prefix: gather them and rank directly
+            unsigned *gk = S.u.h.whist[3];
+#pragma unroll
+            for (int r2 = 0; r2 < PK; ++r2)
+                if (key[r2] && (key[r2] & pmask) == prefix) gk[atomicAdd(&S.gcount, 1)] = key[r2];
+            __syncthreads();
+            const uint32_t mine = (lane < hb) ? gk[lane] : 0u;
+            int gt = 0, ge = 0;
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+                const uint4 v4 = reinterpret_cast<const uint4 *>(gk)[q];
+                const uint32_t vv[4] = {v4.x, v4.y, v4.z, v4.w};
+#pragma unroll
+                for (int c = 0; c < 4; ++c) {
+                    const bool in = 4 * q + c < hb;
+                    gt += (in && vv[c] > mine) ? 1 : 0;
+                    ge += (in && vv[c] >= mine) ? 1 : 0;
+                }
+            }
+            const unsigned long long fm = __ballot(lane < hb && gt < rem && rem <= ge);
+            return (uint32_t)readlane_i((int)mine, fm ? (int)__builtin_ctzll(fm) : 0);
+        }
+    }
+    return prefix;
+}
+
+// Exact threshold and pool from the wave buffers when k <= 64 and every wave
+// buffer holds all its values >= its threshold.  The k-th largest of the 256
+// lanes' maxima is a lower bound L of the k-th largest entry (k distinct
+// entries reach it), so the entries >= L contain the pool.  When they fit two
+// per lane of one wave, wave 0 finds the exact k-th largest key among them
+// with ballot counts (entries below L cannot change it: at least k lie above)
+// and writes the pool (float compare >= T, as the block path does) to
+// S.cval/S.cidx[0, nc).  Returns false, with only scratch changed, when the
+// entries >= L do not fit.  Barriers inside; every thread calls it.
+template <int CAPW, class SM>
+__device__ __forceinline__ bool fast_union_pool(SM &S, int k, float &T, int &nc)
+{
+    const int w = wave_id(), lane = lane_id();
+    const int cnt = S.wcnt[w];
+    const float *bv = S.cval + w * CAPW;
+    const int *bi = S.cidx + w * CAPW;
+    unsigned *lkeys = S.u.h.whist[0];
+    float *gv = S.u.ep + 512;                                // 128 gathered values
+    int *gi = reinterpret_cast<int *>(S.u.ep + 640);         // ... and ids
+    uint32_t lm = 0u;
+    for (int j = lane; j < cnt; j += 64) {
+        const float v = bv[j];
+        if (v == v) lm = max(lm, fkey(v));
+    }
+    lkeys[threadIdx.x] = lm;
+    __syncthreads();
+    // every wave finds the same bound (no broadcast barrier)
+    const uint32_t lq[4] = {lkeys[lane], lkeys[64 + lane], lkeys[128 + lane], lkeys[192 + lane]};
+    const uint32_t L = wave_kth_keys<4>(lq, k);
+    const float lf = L ? keyf(L) : -INFINITY;
+    int mine = 0;
+    for (int j = lane; j < cnt; j += 64) mine += (bv[j] >= lf);
+    int ng = 0;
+    int off = block_excl_scan(mine, ng, S.wsum[0]);
+    if (ng > 128) return false;  // ng is the block total: uniform
+    for (int j = lane; j < cnt; j += 64) {
+        const float v = bv[j];
+        if (v >= lf) {
+            gv[off] = v;
+            gi[off] = bi[j];
+            off++;
+        }
     }
     __syncthreads();
-    return prefix;
+    if (w == 0) {
+        const bool h0 = lane < ng, h1 = lane + 64 < ng;
+        const float v0 = h0 ? gv[lane] : NAN, v1 = h1 ? gv[lane + 64] : NAN;
+        const int i0 = h0 ? gi[lane] : 0, i1 = h1 ? gi[lane + 64] : 0;
+        const uint32_t q[2] = {h0 ? fkey(v0) : 0u, h1 ? fkey(v1) : 0u};
+        const float t = keyf(wave_kth_keys<2>(q, k));
+        const bool p0 = v0 >= t, p1 = v1 >= t;
+        const unsigned long long m0 = __ballot(p0), m1 = __ballot(p1);
+        const int n0 = __popcll(m0);
+        if (p0) {
+            const int pos = lanes_below(m0);
+            S.cval[pos] = v0;
+            S.cidx[pos] = i0;
+        }
+        if (p1) {
+            const int pos = n0 + lanes_below(m1);
+            S.cval[pos] = v1;
+            S.cidx[pos] = i1;
+        }
+        if (lane == 0) {
+            S.sel_digit = n0 + __popcll(m1);
+            S.redf[0] = t;
+        }
+    }
+    __syncthreads();
+    nc = S.sel_digit;
+    T = S.redf[0];
+    return true;
 }
 
 // Block radix select: k-th largest key over the register values v[i] of all
@@ -1306,13 +1453,13 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
         // rank in (probability desc, id asc) order: 64-bit keys, larger first
         const uint64_t key = valid ? (((uint64_t)fkey(p) << 32) | (uint32_t)(63 - lane)) : 0ull;
         uint64_t *kb = reinterpret_cast<uint64_t *>(S.u.ep + 128);
-        kb[lane] = key;
+        kb[lane] = key;  // 0 past the pool: below every valid key
         wave_sync();
         int rank = 0;
-        for (int j = 0; j < nc; j += 2) {
-            const uint64_t k0 = kb[j], k1 = kb[j + 1];
-            rank += (k0 > key);
-            rank += (j + 1 < nc) && (k1 > key);
+#pragma unroll
+        for (int j = 0; j < 64; j += 2) {
+            const ulonglong2 kk = reinterpret_cast<const ulonglong2 *>(kb)[j >> 1];
+            rank += (kk.x > key) + (kk.y > key);
         }
         buf2[lane] = 0.0f;
         wave_sync();
@@ -1521,6 +1668,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         b = gi * 8 + (r & 7);
     }
     if (b >= A.batch) return;
+    // The youngest of the four workgroups resident on a CU loses the vector
+    // memory issue arbitration to the older three (which prefers older waves)
+    // and streams its row ~9% slower, setting the kernel's end; one priority
+    // step for its waves evens the four out.
+    if ((int)blockIdx.x / A.ncu == 3) __builtin_amdgcn_s_setprio(1);
     const int tid = threadIdx.x;
     const int w = wave_id(), lane = lane_id();
     const int V = A.V;
@@ -1553,8 +1705,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     const int vlen = 4 * (se - sb) + (has_extras ? g.head + g.ntail : 0);
     const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
 
-    // the slice sample and the first two iterations' loads go out before the
-    // hash setup
+    // the slice sample goes out first, alone: every workgroup waits for its
+    // sample, and stream loads queued with it would only delay it
     f32x4 smp[SR];
 #pragma unroll
     for (int r = 0; r < SR; ++r) {
@@ -1563,13 +1715,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         smp[r] = (q < se) ? row4[q] : f32x4{NAN, NAN, NAN, NAN};
     }
     f32x4 cur[U4], nx1[U4];
-#pragma unroll
-    for (int u = 0; u < U4; ++u) {
-        const int q = qb + u * 64 + lane;
-        cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
-        const int q1 = qb + WITER + u * 64 + lane;
-        nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
-    }
 
     // ---- setup: hash of history / ban ids, and the threshold estimate ----
     // tau_est = the ks-th largest of the per-thread maxima of the sampled
@@ -1601,6 +1746,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             }
         }
         skeys[tid] = (lm == lm && lm > -INFINITY) ? fkey(lm) : 0u;
+    }
+    // the first two iterations' loads fly during the hash setup and estimate
+#pragma unroll
+    for (int u = 0; u < U4; ++u) {
+        const int q = qb + u * 64 + lane;
+        cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+        const int q1 = qb + WITER + u * 64 + lane;
+        nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
     }
     for (int s = tid; s < HSLOTS; s += WG) {
         S.hkey[s] = -1;
@@ -1761,13 +1914,25 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     // dropped, so the count below verifies it)
     if (use_hash) wave_refine(bv, bi, st.cnt, R, tau_est, false);
     int alive = 0;
-    for (int j = lane; j < st.cnt; j += 64) alive += (bv[j] >= tau_est);
+    uint32_t kx = 0u, kn = 0xFFFFFFFFu;  // range of the live keys
+    for (int j = lane; j < st.cnt; j += 64) {
+        const float v = bv[j];
+        alive += (v >= tau_est);
+        if (v == v) {
+            kx = max(kx, fkey(v));
+            kn = min(kn, fkey(v));
+        }
+    }
     alive = wave_sum(alive);
+    kx = wave_max_u(kx);
+    kn = wave_min_u(kn);
     if (lane == 0) {
         S.wcnt[w] = st.cnt;
         S.walive[w] = alive;
         S.wtau[w] = st.tau;
         S.wstrict[w] = st.strict;
+        S.wkmax[w] = kx;
+        S.wkmin[w] = kn;
     }
     __syncthreads();
     {
@@ -1803,7 +1968,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         float ltau = -INFINITY;
         bool lstrict = false;
         float Ts = -INFINITY;
-        if (tot_s >= k) Ts = keyf(block_kth_union<CAPW>(S, k));
+        if (tot_s >= k) {
+            uint32_t kn, kx;
+            block_key_range(S, kn, kx);
+            Ts = keyf(block_kth_union<CAPW>(S, k, kn, kx));
+        }
         if (strict_s && (tot_s < k || Ts <= tstar_s)) {
             ltau = tstar_s;
             lstrict = true;
@@ -1900,14 +2069,26 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             }
             return;
         }
+        uint32_t kx = 0u, kn = 0xFFFFFFFFu;
         for (int j = 0; j < nsl; ++j) {
             const int o = offs[j];
             const int n = ((j + 1 < nsl) ? offs[j + 1] : ntot) - o;
             const size_t src = ((size_t)b * nsl + j) * A.lcap;
             for (int i = tid; i < n; i += WG) {
-                S.cval[o + i] = dev_load(A.lst_val + src + i);
+                const float v = dev_load(A.lst_val + src + i);
+                S.cval[o + i] = v;
                 S.cidx[o + i] = dev_load(A.lst_idx + src + i);
+                if (v == v) {
+                    kx = max(kx, fkey(v));
+                    kn = min(kn, fkey(v));
+                }
             }
+        }
+        kx = wave_max_u(kx);
+        kn = wave_min_u(kn);
+        if (lane == 0) {
+            S.wkmax[w] = kx;  // partial ranges: only their union is used
+            S.wkmin[w] = kn;
         }
         if (tid < NWAVE) {
             const int c = min(max(ntot - tid * CAPW, 0), CAPW);
@@ -1942,8 +2123,13 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
     float T = -INFINITY;
     bool rescan = false;
-    if (total >= k) {
-        T = keyf(block_kth_union<CAPW>(S, k));
+    int nc = 0, off = 0;
+    const bool pooled = false;
+    if (pooled) {
+    } else if (total >= k) {
+        uint32_t kn, kx;
+        block_key_range(S, kn, kx);
+        T = keyf(block_kth_union<CAPW>(S, k, kn, kx));
         if (any_strict && T <= tstar) {
             T = tstar;
             rescan = true;
@@ -1961,8 +2147,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     // ---- the pool (>= T) of every wave buffer --------------------------
     float rv[PER];
     int ri[PER];
-    int nc = 0, off = 0;
-    if (!rescan) {
+    if (!rescan && !pooled) {
         int mine = 0;
         const int cnt_w = S.wcnt[w];
 #pragma unroll
@@ -1978,34 +2163,33 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 
     if (!rescan) {
         // ---- compact the pool to the front, then sort by id ---------------
-        __syncthreads();
-        int pos = off;
+        if (!pooled) {
+            __syncthreads();
+            int pos = off;
 #pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            if (rv[r] >= T) {
-                S.cval[pos] = rv[r];
-                S.cidx[pos] = ri[r];
-                pos++;
+            for (int r = 0; r < PER; ++r) {
+                if (rv[r] >= T) {
+                    S.cval[pos] = rv[r];
+                    S.cidx[pos] = ri[r];
+                    pos++;
+                }
             }
+            __syncthreads();
         }
-        __syncthreads();
         n_cand = nc;
         if (nc <= 64) {
-            // one candidate per lane of wave 0; ranks against the ids read four
-            // at a time (no barrier)
+            // one candidate per lane of wave 0; ranks against all 64 slots read
+            // four at a time, slots past the pool holding INT_MAX (no barrier)
             if (w == 0) {
                 const float myv = (lane < nc) ? S.cval[lane] : 0.0f;
                 const int myid = (lane < nc) ? S.cidx[lane] : INT_MAX;
+                if (lane >= nc) S.cidx[lane] = INT_MAX;
+                wave_sync();
                 int rank = 0;
 #pragma unroll
                 for (int q4 = 0; q4 < 16; ++q4) {
-                    if (4 * q4 < nc) {
-                        const int4 v = reinterpret_cast<const int4 *>(S.cidx)[q4];
-                        rank += (4 * q4 + 0 < nc && v.x < myid);
-                        rank += (4 * q4 + 1 < nc && v.y < myid);
-                        rank += (4 * q4 + 2 < nc && v.z < myid);
-                        rank += (4 * q4 + 3 < nc && v.w < myid);
-                    }
+                    const int4 v = reinterpret_cast<const int4 *>(S.cidx)[q4];
+                    rank += (v.x < myid) + (v.y < myid) + (v.z < myid) + (v.w < myid);
                 }
                 wave_sync();
                 if (lane < nc) {
@@ -2838,6 +3022,7 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     const int flat = NWAVE * (small ? CAPW_SMALL : CAPW_LARGE);
     A.batch = batch;
     A.nslice = choose_slices(batch, vocab, k_eff, flat);
+    A.ncu = ctx->ncu;
     A.lcap = flat / A.nslice;
     A.lst_val = ctx->lst_val;
     A.lst_idx = ctx->lst_idx;
