@@ -70,7 +70,7 @@ def algorithmic_bytes_per_step(w):
 
 
 class Inputs:
-    def __init__(self, dev, w, seed):
+    def __init__(self, dev, w, seed, packed=True):
         from lal_amd import abi
         lib = dev.lib
         B, V, H = w["B"], w["V"], w["H"]
@@ -86,6 +86,13 @@ class Inputs:
                                                 C.c_float(0.02), dev.stream), "sw")
             abi.check(lib.lal_gpu_synth_normal(abi.ptr(L["x"]), B * n, seed + 7, C.c_float(1.0), dev.stream),
                       "x")
+            L["wpk"] = None
+            if packed:
+                # the load-time weight layout of the matrix-core LM head (the
+                # row-major copy stays for the CPU baseline only)
+                L["wpk"] = dev.alloc(lib.lal_gpu_q8_packed_bytes(V, n))
+                abi.check(lib.lal_gpu_pack_q8(dev.ctx, abi.ptr(L["w"]), V, n, abi.ptr(L["wpk"]), dev.stream),
+                          "pack")
         elif w["kind"] == "zipf":
             abi.check(lib.lal_gpu_synth_zipf(abi.ptr(self.logits), B, V, V, seed, C.c_float(1.1),
                                              C.c_float(0.3), dev.stream), "synth")
@@ -234,6 +241,8 @@ def main():
     ap.add_argument("--workload", default="qwen7b_batched_topk_topp", choices=sorted(WORKLOADS))
     ap.add_argument("--sets", type=int, default=2, help="rotating input sets")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--lm-head-layout", default="packed", choices=("packed", "rowmajor"),
+                    help="weight layout of the Q8 LM head workloads")
     args = ap.parse_args()
 
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -248,7 +257,7 @@ def main():
     w = WORKLOADS[args.workload]
     dev = abi.Device(0, max_batch=w["B"], max_vocab=w["V"])
     nsets = 1 if w["kind"] == "lmhead" else max(1, args.sets)  # W alone exceeds the 256 MB cache
-    sets = [Inputs(dev, w, 1000 + 17 * i) for i in range(nsets)]
+    sets = [Inputs(dev, w, 1000 + 17 * i, packed=args.lm_head_layout == "packed") for i in range(nsets)]
     ios = [s.io(w) for s in sets]
     params = params_for(w)
 
@@ -258,9 +267,15 @@ def main():
             L = inp.lmhead
             abi.check(dev.lib.lal_gpu_quantize_x(dev.ctx, abi.ptr(L["x"]), w["B"], L["n"], 0, abi.ptr(L["xq"]),
                                                  abi.ptr(L["sx"]), dev.stream), "quantize_x")
-            abi.check(dev.lib.lal_gpu_lm_head_q8(dev.ctx, abi.ptr(L["xq"]), abi.ptr(L["sx"]), w["B"], L["n"],
-                                                 abi.ptr(L["w"]), abi.ptr(L["sw"]), w["V"],
-                                                 abi.ptr(inp.logits), w["V"], dev.stream), "lm_head_q8")
+            if L["wpk"] is not None:
+                abi.check(dev.lib.lal_gpu_lm_head_q8_packed(dev.ctx, abi.ptr(L["xq"]), abi.ptr(L["sx"]), w["B"],
+                                                            L["n"], abi.ptr(L["wpk"]), abi.ptr(L["sw"]), w["V"],
+                                                            abi.ptr(inp.logits), w["V"], dev.stream),
+                          "lm_head_q8_packed")
+            else:
+                abi.check(dev.lib.lal_gpu_lm_head_q8(dev.ctx, abi.ptr(L["xq"]), abi.ptr(L["sx"]), w["B"], L["n"],
+                                                     abi.ptr(L["w"]), abi.ptr(L["sw"]), w["V"],
+                                                     abi.ptr(inp.logits), w["V"], dev.stream), "lm_head_q8")
         dev.sample(w["B"], w["V"], params, ios[i % len(ios)])
 
     for i in range(args.warmup):

@@ -23,6 +23,9 @@
  *   lal_gpu_lm_head_q8     runtime/lal_q8_kernel.h:463-543
  *                          lal_lm_head_int8_range[_abs], caller
  *                          tools/server/qwen7b_server.c:829-845
+ *   lal_gpu_pack_q8 +      the same LM head over a weight layout made once
+ *   lal_gpu_lm_head_q8_packed  at load time (qwen7b_server.c:1106-1112 keeps
+ *                          the row-major int8 copy instead)
  *   lal_gpu_uniforms_rand  runtime/lal_sampling.h:116 ((float)rand()/RAND_MAX)
  * The source-compatible drop-in for runtime/lal_sampling.h is
  * include/lal_sampling.h, built on these entry points.
@@ -170,6 +173,22 @@ int  lal_gpu_quantize_x(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
 int  lal_gpu_lm_head_q8(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx,
                         int batch, int n, const int8_t *d_w, const float *d_sw,
                         int vocab, float *d_logits, int ld, void *stream);
+
+/* Packed weight layout for the matrix-core LM head, made once at load time
+ * (the weights are static):  block (T, c), T < ceil(vocab/16), c < ceil(n/64),
+ * is 1024 bytes at offset (T * ceil(n/64) + c) * 1024; its byte 16*l + j
+ * (l < 64, j < 16) holds W[16T + l%16][64c + 16*(l/16) + j], zero past the
+ * matrix.  Each 1 KB block is the B operand of one 16x16x64 int8 MFMA, so a
+ * wave streams its 16 vocab rows as one contiguous run.
+ * lal_gpu_lm_head_q8_packed computes the same logits as lal_gpu_lm_head_q8
+ * (bit for bit) from that layout; it needs n % 16 == 0 and 16-byte aligned
+ * d_xq / d_wpk. */
+size_t lal_gpu_q8_packed_bytes(int vocab, int n);
+int  lal_gpu_pack_q8(lal_gpu_ctx *ctx, const int8_t *d_w, int vocab, int n, int8_t *d_wpk,
+                     void *stream);
+int  lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx,
+                               int batch, int n, const int8_t *d_wpk, const float *d_sw,
+                               int vocab, float *d_logits, int ld, void *stream);
 
 /* Host helper: srand(seed) then n draws of (float)rand()/(float)RAND_MAX
  * (gpt2 != 0: (float)(rand()%1000000)/1000000.0f), the reference's RNG

@@ -68,6 +68,9 @@ EXPORTS = [
     ("lal_gpu_sample_finish", _i, [_vp, _i, _i, C.POINTER(SampleParams), C.POINTER(FinishIO), _vp]),
     ("lal_gpu_quantize_x", _i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     ("lal_gpu_lm_head_q8", _i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
+    ("lal_gpu_q8_packed_bytes", _sz, [_i, _i]),
+    ("lal_gpu_pack_q8", _i, [_vp, _vp, _i, _i, _vp, _vp]),
+    ("lal_gpu_lm_head_q8_packed", _i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
     ("lal_gpu_uniforms_rand", None, [_u, _i, C.POINTER(_f), _i]),
     ("lal_gpu_malloc", _i, [C.POINTER(_vp), _sz]),
     ("lal_gpu_free", _i, [_vp]),

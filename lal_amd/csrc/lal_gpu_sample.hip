@@ -554,52 +554,6 @@ __device__ __forceinline__ uint32_t wave_kth_lane_key(uint32_t key, int k)
     return K;
 }
 
-// k-th largest of the keys q[0..NQ) held by the wave's lanes (key 0 = none):
-// the largest K with at least k keys >= K, 0 when fewer than k are nonzero.
-// The bits above the highest one where the largest and smallest nonzero keys
-// differ are common to every candidate; the rest are decided two at a time
-// (three independent ballot counts per step).  Wave-synchronous.
-template <int NQ>
-__device__ __forceinline__ int ballot_count_ge(const uint32_t (&q)[NQ], uint32_t c)
-{
-    int n = 0;
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) n += __popcll(__ballot(q[i] >= c));
-    return n;
-}
-
-template <int NQ>
-__device__ __forceinline__ uint32_t wave_kth_keys(const uint32_t (&q)[NQ], int k)
-{
-    uint32_t mx = 0u, mn = 0xFFFFFFFFu;
-    int nz = 0;
-#pragma unroll
-    for (int i = 0; i < NQ; ++i) {
-        mx = max(mx, q[i]);
-        if (q[i]) mn = min(mn, q[i]);
-        nz += __popcll(__ballot(q[i] != 0u));
-    }
-    if (nz < k) return 0u;
-    mx = wave_max_u(mx);
-    mn = wave_min_u(mn);
-    if (mn >= mx) return mx;
-    int bit = 31 - __builtin_clz(mn ^ mx);  // highest differing bit
-    uint32_t K = (bit == 31) ? 0u : (mx & ~((2u << bit) - 1u));
-    if (!(bit & 1)) {  // odd number of bits left: one single step
-        const uint32_t c = K | (1u << bit);
-        if (ballot_count_ge<NQ>(q, c) >= k) K = c;
-        --bit;
-    }
-    for (; bit >= 1; bit -= 2) {
-        const uint32_t c1 = K | (1u << (bit - 1)), c2 = K | (2u << (bit - 1)),
-                       c3 = K | (3u << (bit - 1));
-        const int n1 = ballot_count_ge<NQ>(q, c1), n2 = ballot_count_ge<NQ>(q, c2),
-                  n3 = ballot_count_ge<NQ>(q, c3);
-        K = (n3 >= k) ? c3 : (n2 >= k) ? c2 : (n1 >= k) ? c1 : K;
-    }
-    return K;
-}
-
 // ---------------------------------------------------------------------------
 // Per-wave state and candidate buffer
 // ---------------------------------------------------------------------------
@@ -927,80 +881,6 @@ __device__ __forceinline__ uint32_t block_kth_union(SM &S, int k, uint32_t kmin,
         }
     }
     return prefix;
-}
-
-// Exact threshold and pool from the wave buffers when k <= 64 and every wave
-// buffer holds all its values >= its threshold.  The k-th largest of the 256
-// lanes' maxima is a lower bound L of the k-th largest entry (k distinct
-// entries reach it), so the entries >= L contain the pool.  When they fit two
-// per lane of one wave, wave 0 finds the exact k-th largest key among them
-// with ballot counts (entries below L cannot change it: at least k lie above)
-// and writes the pool (float compare >= T, as the block path does) to
-// S.cval/S.cidx[0, nc).  Returns false, with only scratch changed, when the
-// entries >= L do not fit.  Barriers inside; every thread calls it.
-template <int CAPW, class SM>
-__device__ __forceinline__ bool fast_union_pool(SM &S, int k, float &T, int &nc)
-{
-    const int w = wave_id(), lane = lane_id();
-    const int cnt = S.wcnt[w];
-    const float *bv = S.cval + w * CAPW;
-    const int *bi = S.cidx + w * CAPW;
-    unsigned *lkeys = S.u.h.whist[0];
-    float *gv = S.u.ep + 512;                                // 128 gathered values
-    int *gi = reinterpret_cast<int *>(S.u.ep + 640);         // ... and ids
-    uint32_t lm = 0u;
-    for (int j = lane; j < cnt; j += 64) {
-        const float v = bv[j];
-        if (v == v) lm = max(lm, fkey(v));
-    }
-    lkeys[threadIdx.x] = lm;
-    __syncthreads();
-    // every wave finds the same bound (no broadcast barrier)
-    const uint32_t lq[4] = {lkeys[lane], lkeys[64 + lane], lkeys[128 + lane], lkeys[192 + lane]};
-    const uint32_t L = wave_kth_keys<4>(lq, k);
-    const float lf = L ? keyf(L) : -INFINITY;
-    int mine = 0;
-    for (int j = lane; j < cnt; j += 64) mine += (bv[j] >= lf);
-    int ng = 0;
-    int off = block_excl_scan(mine, ng, S.wsum[0]);
-    if (ng > 128) return false;  // ng is the block total: uniform
-    for (int j = lane; j < cnt; j += 64) {
-        const float v = bv[j];
-        if (v >= lf) {
-            gv[off] = v;
-            gi[off] = bi[j];
-            off++;
-        }
-    }
-    __syncthreads();
-    if (w == 0) {
-        const bool h0 = lane < ng, h1 = lane + 64 < ng;
-        const float v0 = h0 ? gv[lane] : NAN, v1 = h1 ? gv[lane + 64] : NAN;
-        const int i0 = h0 ? gi[lane] : 0, i1 = h1 ? gi[lane + 64] : 0;
-        const uint32_t q[2] = {h0 ? fkey(v0) : 0u, h1 ? fkey(v1) : 0u};
-        const float t = keyf(wave_kth_keys<2>(q, k));
-        const bool p0 = v0 >= t, p1 = v1 >= t;
-        const unsigned long long m0 = __ballot(p0), m1 = __ballot(p1);
-        const int n0 = __popcll(m0);
-        if (p0) {
-            const int pos = lanes_below(m0);
-            S.cval[pos] = v0;
-            S.cidx[pos] = i0;
-        }
-        if (p1) {
-            const int pos = n0 + lanes_below(m1);
-            S.cval[pos] = v1;
-            S.cidx[pos] = i1;
-        }
-        if (lane == 0) {
-            S.sel_digit = n0 + __popcll(m1);
-            S.redf[0] = t;
-        }
-    }
-    __syncthreads();
-    nc = S.sel_digit;
-    T = S.redf[0];
-    return true;
 }
 
 // Block radix select: k-th largest key over the register values v[i] of all
@@ -2124,9 +2004,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     float T = -INFINITY;
     bool rescan = false;
     int nc = 0, off = 0;
-    const bool pooled = false;
-    if (pooled) {
-    } else if (total >= k) {
+    if (total >= k) {
         uint32_t kn, kx;
         block_key_range(S, kn, kx);
         T = keyf(block_kth_union<CAPW>(S, k, kn, kx));
@@ -2147,7 +2025,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     // ---- the pool (>= T) of every wave buffer --------------------------
     float rv[PER];
     int ri[PER];
-    if (!rescan && !pooled) {
+    if (!rescan) {
         int mine = 0;
         const int cnt_w = S.wcnt[w];
 #pragma unroll
@@ -2163,19 +2041,17 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 
     if (!rescan) {
         // ---- compact the pool to the front, then sort by id ---------------
-        if (!pooled) {
-            __syncthreads();
-            int pos = off;
+        __syncthreads();
+        int pos = off;
 #pragma unroll
-            for (int r = 0; r < PER; ++r) {
-                if (rv[r] >= T) {
-                    S.cval[pos] = rv[r];
-                    S.cidx[pos] = ri[r];
-                    pos++;
-                }
+        for (int r = 0; r < PER; ++r) {
+            if (rv[r] >= T) {
+                S.cval[pos] = rv[r];
+                S.cidx[pos] = ri[r];
+                pos++;
             }
-            __syncthreads();
         }
+        __syncthreads();
         n_cand = nc;
         if (nc <= 64) {
             // one candidate per lane of wave 0; ranks against all 64 slots read
@@ -2667,6 +2543,154 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_mfma_kernel(const int8
     }
 }
 
+// Int8 LM head over the packed weight layout (lal_gpu_pack_q8): block (T, c)
+// = 1024 bytes holding w[16T + l%16][64c + 16(l/16) + j] at byte 16 l + j, the
+// B operand of one v_mfma_i32_16x16x64_i8 as its 64 lanes load it, so every
+// wave streams its 16 vocab rows as one contiguous run (n_pad bytes per row,
+// 1 KB per load instruction).  Same arithmetic and A/C layouts as
+// lm_head_mfma_kernel; a workgroup's tiles of 16 rows (one per wave at a time)
+// and their passes of 256 k-bytes form one flat sequence of steps with two
+// steps of w in flight across tile boundaries; the activations of a step are
+// staged in LDS one step ahead, their global loads issued before the w loads
+// of the same step (loads complete in issue order).  Batch rows 1..64.
+template <int MT>
+__global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const int8_t *xq, const float *sx, int n,
+                                                                        const int8_t *wpk, const float *sw, int V,
+                                                                        float *logits, int ld, int b0, int nb)
+{
+    __shared__ __align__(16) int8_t xs[2][MT * 16 * LMM_KC];
+    constexpr int XCH = MT * 16 * (LMM_KC / 16);
+    constexpr int XPT = (XCH + 64 * LMM_WAVES - 1) / (64 * LMM_WAVES);
+    const int wv = wave_id(), lane = lane_id(), tid = threadIdx.x;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int npass = (n + LMM_KC - 1) / LMM_KC;
+    const int nc64 = (n + 63) / 64;           // 1 KB blocks per 16-row tile
+    const int ntile = (V + 15) / 16;
+    // this workgroup's tiles: [tlo, thi); wave wv takes tlo + wv, tlo + wv + 4, ...
+    const int tlo = (int)(((long long)ntile * blockIdx.x) / gridDim.x);
+    const int thi = (int)(((long long)ntile * (blockIdx.x + 1)) / gridDim.x);
+    const int nround = (thi - tlo + LMM_WAVES - 1) / LMM_WAVES;
+    const int nstep = nround * npass;
+    if (nstep == 0) return;
+
+    auto fetch_x = [&](v4i (&xr)[XPT], int p) {
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int c = tid + j * 64 * LMM_WAVES;
+            const int row = c / (LMM_KC / 16), col = (c % (LMM_KC / 16)) * 16;
+            const int k = p * LMM_KC + col;
+            v4i v = {0, 0, 0, 0};
+            if (c < XCH && row < nb && k < n) v = *reinterpret_cast<const v4i *>(xq + (size_t)(b0 + row) * n + k);
+            xr[j] = v;
+        }
+    };
+    // staged in A-operand order: the 16 bytes lane l of wave-instruction
+    // (mt, s4) reads sit at ((mt*4 + s4)*64 + l)*16, so each read is one
+    // contiguous 1 KB (no bank conflicts)
+    auto stage_x = [&](const v4i (&xr)[XPT], int buf) {
+#pragma unroll
+        for (int j = 0; j < XPT; ++j) {
+            const int c = tid + j * 64 * LMM_WAVES;
+            if (c < XCH) {
+                const int row = c / (LMM_KC / 16), c16 = c % (LMM_KC / 16);
+                const int dst = (((row >> 4) * 4 + (c16 >> 2)) * 64 + (c16 & 3) * 16 + (row & 15)) * 16;
+                *reinterpret_cast<v4i *>(&xs[buf][dst]) = xr[j];
+            }
+        }
+    };
+    // w of (round r, pass p): this wave's tile, blocks 4p .. 4p+3
+    auto fetch_w = [&](v4i (&f)[4], int r, int p) {
+        const int T = tlo + r * LMM_WAVES + wv;
+        const bool ok = r < nround && T < thi;
+        const v4i *base = reinterpret_cast<const v4i *>(wpk + ((size_t)(ok ? T : 0) * nc64) * 1024) + lane;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const int c = 4 * p + s4;
+            f[s4] = (ok && c < nc64) ? __builtin_nontemporal_load(base + (size_t)c * 64) : v4i{0, 0, 0, 0};
+        }
+    };
+
+    v4i acc[MT];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+    v4i w0[4], w1[4], w2[4];
+    v4i xr[XPT];
+    fetch_x(xr, 0);
+    stage_x(xr, 0);
+    fetch_x(xr, 1 % npass);  // activations of step 1, ahead of every w load
+    fetch_w(w0, 0, 0);
+    int rw = (npass > 1) ? 0 : 1, pw = (npass > 1) ? 1 : 0;  // position of step 1
+    fetch_w(w1, rw, pw);
+    if (++pw == npass) { pw = 0; ++rw; }                   // position of step 2
+    int r = 0, p = 0;                                        // position of step s
+    for (int s = 0; s < nstep; ++s) {
+        __syncthreads();  // step s's activations are in; the other buffer is free
+        if (s + 1 < nstep) {
+            stage_x(xr, (s + 1) & 1);
+            if (s + 2 < nstep) fetch_x(xr, pw);
+        }
+        fetch_w(w2, rw, pw);
+        if (++pw == npass) { pw = 0; ++rw; }
+        const int8_t *xb = xs[s & 1];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const v4i a = *reinterpret_cast<const v4i *>(xb + ((mt * 4 + s4) * 64 + lane) * 16);
+                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w0[s4], acc[mt], 0, 0, 0);
+            }
+        }
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            w0[s4] = w1[s4];
+            w1[s4] = w2[s4];
+        }
+        if (++p == npass) {  // the tile's dot products are complete
+            const int T = tlo + r * LMM_WAVES + wv;
+            const int v = 16 * T + r16;
+            if (T < thi && v < V) {
+                const float swv = sw[v];
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+                    for (int i = 0; i < 4; ++i) {
+                        const int bb = mt * 16 + 4 * g + i;
+                        if (bb < nb) logits[(size_t)(b0 + bb) * ld + v] = (sx[b0 + bb] * swv) * (float)acc[mt][i];
+                    }
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+            p = 0;
+            ++r;
+        }
+    }
+}
+
+// Row-major int8 [V][n] -> packed layout (one thread per 16 bytes).
+__global__ __launch_bounds__(256) void pack_q8_kernel(const int8_t *w, int V, int n, int8_t *wpk)
+{
+    const int nc64 = (n + 63) / 64;
+    const size_t nblk = (size_t)((V + 15) / 16) * nc64;
+    const size_t i = (size_t)blockIdx.x * 256 + threadIdx.x;  // 16-byte unit
+    if (i >= nblk * 64) return;
+    const size_t blk = i >> 6;
+    const int l = (int)(i & 63);
+    const int T = (int)(blk / nc64), c = (int)(blk % nc64);
+    const int v = 16 * T + (l & 15), k0 = 64 * c + 16 * (l >> 4);
+    v4i out = {0, 0, 0, 0};
+    if (v < V) {
+        if (((n & 15) == 0) && k0 + 16 <= n) {
+            out = *reinterpret_cast<const v4i *>(w + (size_t)v * n + k0);
+        } else {
+            int8_t b[16];
+#pragma unroll
+            for (int j = 0; j < 16; ++j) b[j] = (k0 + j < n) ? w[(size_t)v * n + k0 + j] : (int8_t)0;
+            out = *reinterpret_cast<const v4i *>(b);
+        }
+    }
+    *reinterpret_cast<v4i *>(wpk + i * 16) = out;
+}
+
 // Rows whose length is not a multiple of 16 bytes: one wave per vocab row,
 // byte loads, same exact int32 accumulation.
 __global__ __launch_bounds__(256) void lm_head_scalar_kernel(const int8_t *xq, const float *sx, int n,
@@ -3128,6 +3152,52 @@ int lal_gpu_lm_head_q8(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx, 
         case 6: hipLaunchKernelGGL(lm_head_dot4_kernel<6>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
         case 7: hipLaunchKernelGGL(lm_head_dot4_kernel<7>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
         default: hipLaunchKernelGGL(lm_head_dot4_kernel<8>, grid, block, 0, s, d_xq, d_sx, n, d_w, d_sw, vocab, d_logits, ld, b0); break;
+        }
+        LAL_HIP(hipGetLastError());
+    }
+    return LAL_GPU_OK;
+}
+
+size_t lal_gpu_q8_packed_bytes(int vocab, int n)
+{
+    if (vocab <= 0 || n <= 0) return 0;
+    return (size_t)((vocab + 15) / 16) * (size_t)((n + 63) / 64) * 1024u;
+}
+
+int lal_gpu_pack_q8(lal_gpu_ctx *ctx, const int8_t *d_w, int vocab, int n, int8_t *d_wpk, void *stream)
+{
+    if (!ctx || !d_w || !d_wpk || vocab <= 0 || n <= 0) return LAL_GPU_E_INVAL;
+    if ((uintptr_t)d_wpk & 15) return LAL_GPU_E_INVAL;
+    const size_t units = lal_gpu_q8_packed_bytes(vocab, n) / 16;
+    const size_t nblk = (units + 255) / 256;
+    if (nblk > 0x7fffffffu) return LAL_GPU_E_RANGE;
+    hipLaunchKernelGGL(pack_q8_kernel, dim3((unsigned)nblk), dim3(256), 0, (hipStream_t)stream, d_w, vocab, n,
+                       d_wpk);
+    LAL_HIP(hipGetLastError());
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx, int batch, int n,
+                              const int8_t *d_wpk, const float *d_sw, int vocab, float *d_logits, int ld,
+                              void *stream)
+{
+    if (!ctx || !d_xq || !d_sx || !d_wpk || !d_sw || !d_logits) return LAL_GPU_E_INVAL;
+    if (batch <= 0 || n <= 0 || vocab <= 0 || ld < vocab) return LAL_GPU_E_INVAL;
+    if (((uintptr_t)d_xq & 15) || ((uintptr_t)d_wpk & 15) || (n & 15)) return LAL_GPU_E_INVAL;
+    hipStream_t s = (hipStream_t)stream;
+    const int ntile = (vocab + 15) / 16;
+    for (int b0 = 0; b0 < batch; b0 += LMM_MAXB) {
+        const int nb = std::min(LMM_MAXB, batch - b0);
+        const int mt = (nb + 15) / 16;
+        int per_cu = (mt <= 2) ? 4 : 2;  // workgroups per CU (measured best at each tile height)
+        if (const char *env = getenv("LAL_GPU_LMH_WG")) per_cu = std::max(1, atoi(env));
+        const unsigned nwg = (unsigned)std::max(1, std::min(per_cu * ctx->ncu, (ntile + LMM_WAVES - 1) / LMM_WAVES));
+        const dim3 g2(nwg), blk(64 * LMM_WAVES);
+        switch (mt) {
+        case 1: hipLaunchKernelGGL(lm_head_packed_kernel<1>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb); break;
+        case 2: hipLaunchKernelGGL(lm_head_packed_kernel<2>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb); break;
+        case 3: hipLaunchKernelGGL(lm_head_packed_kernel<3>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb); break;
+        default: hipLaunchKernelGGL(lm_head_packed_kernel<4>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb); break;
         }
         LAL_HIP(hipGetLastError());
     }

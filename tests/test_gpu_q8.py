@@ -64,6 +64,35 @@ def lm_head(dev, xq, sx, W, sw, ld=None, offset=0):
     return out
 
 
+def packed_layout(W):
+    """The packed layout as include/lal_gpu_sample.h defines it, in numpy:
+    block (T, c) byte 16*l + j = W[16T + l%16][64c + 16*(l//16) + j]."""
+    V, n = W.shape
+    NT, NC = (V + 15) // 16, (n + 63) // 64
+    Wp = np.zeros((NT * 16, NC * 64), np.int8)
+    Wp[:V, :n] = W
+    return Wp.reshape(NT, 16, NC, 4, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
+
+
+def lm_head_packed(dev, xq, sx, W, sw):
+    from lal_amd import abi
+    B, n = xq.shape
+    V = W.shape[0]
+    nbytes = dev.lib.lal_gpu_q8_packed_bytes(V, n)
+    dW, dP = dev.put(np.ascontiguousarray(W)), dev.alloc(nbytes)
+    abi.check(dev.lib.lal_gpu_pack_q8(dev.ctx, dW.ptr, V, n, dP.ptr, dev.stream), "pack")
+    dq, ds, dsw = dev.put(np.ascontiguousarray(xq)), dev.put(np.asarray(sx, np.float32)), dev.put(sw)
+    dl = dev.alloc(4 * B * V)
+    abi.check(dev.lib.lal_gpu_lm_head_q8_packed(dev.ctx, dq.ptr, ds.ptr, B, n, dP.ptr, dsw.ptr, V, dl.ptr,
+                                                V, dev.stream), "lm_head_packed")
+    dev.sync()
+    out = dl.download((B, V), np.float32)
+    packed = dP.download(nbytes, np.int8)
+    for b in (dW, dP, dq, ds, dsw, dl):
+        b.close()
+    return out, packed
+
+
 def test_quantize_x_golden(dev):
     for rec in golden_cases.load()["q8"]["quantize_x"]:
         x = (synth.normal(rec["seed"], 0, rec["n"]) * np.float32(rec["scale"])).astype(np.float32)
@@ -141,3 +170,67 @@ def test_lm_head_matrix_core_path(dev, orc, B):
         want = orc.lm_head(q[b].copy(), s[b], W, sw)
         assert np.array_equal(out[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
     log(f"matrix-core lm_head B={B}: {B} x {V} bit-exact")
+
+
+@pytest.mark.parametrize("B", [1, 3, 9, 16, 33, 64, 100])
+def test_lm_head_packed(dev, orc, B):
+    """The packed weight layout (lal_gpu_pack_q8) against its definition, and
+    lal_gpu_lm_head_q8_packed bit-exact against the oracle on every logit
+    (V = 5003 leaves a partial 16-row tile, n = 3392 a partial 256-byte pass)."""
+    V, n = 5003, 3392
+    rng = np.random.default_rng(1000 + B)
+    W = rng.integers(-127, 128, (V, n)).astype(np.int8)
+    sw = (rng.random(V) * 0.019 + 0.001).astype(np.float32)
+    x = synth.normal(170 + B, 0, B * n).reshape(B, n).astype(np.float32)
+    s, q = quantize(dev, x, 0)
+    out, packed = lm_head_packed(dev, q, s, W, sw)
+    assert np.array_equal(packed, packed_layout(W)), "packed layout"
+    for b in range(B):
+        want = orc.lm_head(q[b].copy(), s[b], W, sw)
+        assert np.array_equal(out[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
+    log(f"packed lm_head B={B}: {B} x {V} bit-exact")
+
+
+def test_pack_layout_ragged(dev):
+    """Shapes that are not multiples of 16 rows or 64 bytes pack with zeros."""
+    for V, n in ((1, 16), (17, 80), (37, 200), (5, 1000)):
+        W = np.random.default_rng(V * n).integers(-127, 128, (V, n)).astype(np.int8)
+        from lal_amd import abi
+        nbytes = dev.lib.lal_gpu_q8_packed_bytes(V, n)
+        assert nbytes == ((V + 15) // 16) * ((n + 63) // 64) * 1024
+        dW, dP = dev.put(W), dev.alloc(nbytes)
+        abi.check(dev.lib.lal_gpu_pack_q8(dev.ctx, dW.ptr, V, n, dP.ptr, dev.stream), "pack")
+        dev.sync()
+        assert np.array_equal(dP.download(nbytes, np.int8), packed_layout(W)), f"V={V} n={n}"
+        dW.close()
+        dP.close()
+
+
+@pytest.mark.parametrize("B", [1, 16, 64])
+def test_lm_head_packed_qwen7b_shape(dev, B):
+    """Qwen-7B shape: the packed path equals the row-major path bit for bit
+    (the row-major path is checked against the oracle above)."""
+    from lal_amd import abi
+    V, n = 152064, 3584
+    x = synth.normal(90 + B, 0, B * n).reshape(B, n).astype(np.float32)
+    s, q = quantize(dev, x, 0)
+    dW = dev.alloc(V * n)
+    abi.check(dev.lib.lal_gpu_synth_int8(dW.ptr, V * n, 91, -127, 127, dev.stream), "synth W")
+    dsw = dev.alloc(4 * V)
+    abi.check(dev.lib.lal_gpu_synth_uniform(dsw.ptr, V, 92, C.c_float(0.001), C.c_float(0.02),
+                                            dev.stream), "synth sw")
+    nbytes = dev.lib.lal_gpu_q8_packed_bytes(V, n)
+    dP = dev.alloc(nbytes)
+    abi.check(dev.lib.lal_gpu_pack_q8(dev.ctx, dW.ptr, V, n, dP.ptr, dev.stream), "pack")
+    dq, ds = dev.put(q), dev.put(s)
+    d1, d2 = dev.alloc(4 * B * V), dev.alloc(4 * B * V)
+    abi.check(dev.lib.lal_gpu_lm_head_q8(dev.ctx, dq.ptr, ds.ptr, B, n, dW.ptr, dsw.ptr, V, d1.ptr, V,
+                                         dev.stream), "lm_head")
+    abi.check(dev.lib.lal_gpu_lm_head_q8_packed(dev.ctx, dq.ptr, ds.ptr, B, n, dP.ptr, dsw.ptr, V, d2.ptr,
+                                                V, dev.stream), "lm_head_packed")
+    dev.sync()
+    a, b = d1.download((B, V), np.float32), d2.download((B, V), np.float32)
+    assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
+    log(f"packed lm_head B={B}: {B} x {V} equal to the row-major path")
+    for bb in (dW, dsw, dP, dq, ds, d1, d2):
+        bb.close()
