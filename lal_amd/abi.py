@@ -12,6 +12,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "liblal_gpu.so")
 
+E_INVAL, E_RANGE, E_HIP, E_NOMEM, E_NODEV = -1, -2, -3, -4, -5
 VARIANT_BASIC = 0
 VARIANT_FILTERED = 1
 F_WRITEBACK = 0x1
@@ -48,6 +49,13 @@ class SampleIO(C.Structure):
                 ("cand_vals", C.c_void_p)]
 
 
+class Gpq8Tensor(C.Structure):
+    """lal_gpq8_tensor (include/lal_gpq8.h)."""
+    _fields_ = [("key", C.c_char_p), ("ndim", C.c_int), ("shape", C.c_int * 4), ("qtype", C.c_int),
+                ("data_len", C.c_uint64), ("data", C.c_void_p), ("n_scale", C.c_int),
+                ("scale", C.c_void_p)]
+
+
 class FinishIO(C.Structure):
     _fields_ = [("n_cand", C.c_void_p), ("cand_ld", C.c_int), ("cand_ids", C.c_void_p),
                 ("cand_vals", C.c_void_p), ("keep", C.c_void_p), ("uniforms", C.c_void_p),
@@ -69,6 +77,13 @@ EXPORTS = [
     ("lal_gpu_quantize_x", _i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     ("lal_gpu_lm_head_q8", _i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
     ("lal_gpu_q8_packed_bytes", _sz, [_i, _i]),
+    ("lal_gpu_quantize_w_q8", _i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp]),
+    ("lal_gpq8_open", _i, [C.c_char_p, C.POINTER(_vp)]),
+    ("lal_gpq8_close", None, [_vp]),
+    ("lal_gpq8_count", _i, [_vp]),
+    ("lal_gpq8_tensor_at", _i, [_vp, _i, C.POINTER(Gpq8Tensor)]),
+    ("lal_gpq8_find", _i, [_vp, C.c_char_p, C.POINTER(Gpq8Tensor)]),
+    ("lal_gpu_load_lm_head", _i, [_vp, _vp, C.c_char_p, _vp, _vp, C.POINTER(_i), C.POINTER(_i), _vp]),
     ("lal_gpu_pack_q8", _i, [_vp, _vp, _i, _i, _vp, _vp]),
     ("lal_gpu_lm_head_q8_packed", _i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
     ("lal_gpu_uniforms_rand", None, [_u, _i, C.POINTER(_f), _i]),

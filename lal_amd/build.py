@@ -26,10 +26,10 @@ def run(cmd, **kw):
 
 
 def build_gpu_lib():
-    src = os.path.join(HERE, "csrc", "lal_gpu_sample.hip")
+    srcs = [os.path.join(HERE, "csrc", "lal_gpu_sample.hip"), os.path.join(HERE, "csrc", "lal_gpq8.cpp")]
     out = os.path.join(HERE, "liblal_gpu.so")
     tmp = out + ".tmp"
-    run([HIPCC] + HIP_FLAGS + ["-o", tmp, src])
+    run([HIPCC] + HIP_FLAGS + ["-o", tmp] + srcs)
     os.replace(tmp, out)
     return out
 

@@ -35,6 +35,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include "lal_gpq8.h"
 #include "lal_gpu_sample.h"
 #include "lal_gpu_workload.h"
 
@@ -2666,6 +2667,33 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
     }
 }
 
+// Startup weight quantizer (runtime/lal_q8_kernel.h:357-372,
+// lal_quantize_q8_per_row): per row, scale = max|w| / 127 (at least 1e-8),
+// q = lroundf(w * (1/scale)) clamped to [-127, 127] (round half away from
+// zero).  One workgroup per row; the maximum is order-free.
+__global__ __launch_bounds__(256) void quantize_w_kernel(const float *w, int n, int8_t *q, float *scale)
+{
+    __shared__ float red[4];
+    const int j = blockIdx.x;
+    const float *r = w + (size_t)j * n;
+    float m = 0.0f;
+    for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(r[i]));
+    m = wave_max(m);
+    if (lane_id() == 0) red[wave_id()] = m;
+    __syncthreads();
+    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    float s = m / 127.0f;
+    if (s < 1e-8f) s = 1e-8f;
+    const float inv = 1.0f / s;
+    for (int i = threadIdx.x; i < n; i += 256) {
+        const float t = r[i] * inv;
+        int v = (int)roundf(t);
+        v = min(127, max(-127, v));
+        q[(size_t)j * n + i] = (int8_t)v;
+    }
+    if (threadIdx.x == 0) scale[j] = s;
+}
+
 // Row-major int8 [V][n] -> packed layout (one thread per 16 bytes).
 __global__ __launch_bounds__(256) void pack_q8_kernel(const int8_t *w, int V, int n, int8_t *wpk)
 {
@@ -3175,6 +3203,25 @@ int lal_gpu_pack_q8(lal_gpu_ctx *ctx, const int8_t *d_w, int vocab, int n, int8_
                        d_wpk);
     LAL_HIP(hipGetLastError());
     return LAL_GPU_OK;
+}
+
+int lal_gpu_quantize_w_q8(lal_gpu_ctx *ctx, const float *d_w, int vocab, int n, int8_t *d_wq, int8_t *d_wpk,
+                          float *d_sw, void *stream)
+{
+    if (!ctx || !d_w || !d_sw || vocab <= 0 || n <= 0 || (!d_wq && !d_wpk)) return LAL_GPU_E_INVAL;
+    if (d_wpk && ((uintptr_t)d_wpk & 15)) return LAL_GPU_E_INVAL;
+    hipStream_t s = (hipStream_t)stream;
+    int8_t *q = d_wq;
+    if (!q) LAL_HIP(hipMallocAsync((void **)&q, (size_t)vocab * n, s));
+    hipLaunchKernelGGL(quantize_w_kernel, dim3(vocab), dim3(256), 0, s, d_w, n, q, d_sw);
+    hipError_t e = hipGetLastError();
+    int rc = (e == hipSuccess) ? LAL_GPU_OK : hip_fail(e);
+    if (rc == LAL_GPU_OK && d_wpk) rc = lal_gpu_pack_q8(ctx, q, vocab, n, d_wpk, stream);
+    if (!d_wq) {
+        const hipError_t f = hipFreeAsync(q, s);
+        if (rc == LAL_GPU_OK && f != hipSuccess) rc = hip_fail(f);
+    }
+    return rc;
 }
 
 int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx, int batch, int n,

@@ -7,13 +7,13 @@ import re
 import pytest
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADERS = ["include/lal_gpu_sample.h", "include/lal_gpu_workload.h"]
+HEADERS = ["include/lal_gpu_sample.h", "include/lal_gpu_workload.h", "include/lal_gpq8.h"]
 
 
 def declared(path):
     text = open(os.path.join(ROOT, path)).read()
     text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return sorted(set(re.findall(r"\b(lal_gpu_\w+)\s*\(", text)))
+    return sorted(set(re.findall(r"\b(lal_(?:gpu|gpq8)_\w+)\s*\(", text)))
 
 
 def test_library_exports_every_declared_symbol():
@@ -45,6 +45,15 @@ def test_struct_layouts_match_header():
         body = re.search(r"typedef struct " + cname + r"\s*\{(.*?)\}", text, re.S).group(1)
         names = re.findall(r"\**(\w+)\s*;", body)
         assert names == [f for f, _ in py._fields_], cname
+
+
+def test_gpq8_tensor_layout_matches_header():
+    from lal_amd import abi
+    text = open(os.path.join(ROOT, "include/lal_gpq8.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    body = re.search(r"typedef struct lal_gpq8_tensor\s*\{(.*?)\}", text, re.S).group(1)
+    names = re.findall(r"\**(\w+)(?:\[\w+\])?\s*;", body)
+    assert names == [f for f, _ in abi.Gpq8Tensor._fields_]
 
 
 def test_no_device_calls_without_gpu():
