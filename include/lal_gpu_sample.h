@@ -23,6 +23,8 @@
  *   lal_gpu_lm_head_q8     runtime/lal_q8_kernel.h:463-543
  *                          lal_lm_head_int8_range[_abs], caller
  *                          tools/server/qwen7b_server.c:829-845
+ *   lal_gpu_lm_head_rerank tools/server/gpt2_server.c:2155-2215, the fp32
+ *                          re-score of the int8 LM head's top 512
  *   lal_gpu_pack_q8 +      the same LM head over a weight layout made once
  *   lal_gpu_lm_head_q8_packed  at load time (qwen7b_server.c:1106-1112 keeps
  *                          the row-major int8 copy instead)
@@ -189,6 +191,19 @@ int  lal_gpu_pack_q8(lal_gpu_ctx *ctx, const int8_t *d_w, int vocab, int n, int8
 int  lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx,
                                int batch, int n, const int8_t *d_wpk, const float *d_sw,
                                int vocab, float *d_logits, int ld, void *stream);
+
+/* GPT-2 int8 LM head, pass 2 (tools/server/gpt2_server.c:2155-2215): d_logits
+ * holds pass 1 (lal_gpu_lm_head_q8 over wte rows quantized by
+ * lal_gpu_quantize_x mode 1, as gpt2_server.c:3752-3761 does at load).  The
+ * rerank_n (<= 512; the reference uses 512) largest logits of each row -- the
+ * set the reference's min-heap keeps, ties at the boundary included -- are
+ * re-scored in fp32 from the hidden state d_x [batch][n] (n <= 8192):
+ * w = (float)wq[v][i] * ws[v], eight fused multiply-add lanes over i mod 8
+ * summed in lane order, then the tail (the AVX2 build's order), written in
+ * place; every other logit keeps its int8 value. */
+int  lal_gpu_lm_head_rerank(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
+                            const int8_t *d_wq, const float *d_ws, int vocab, int rerank_n,
+                            float *d_logits, int ld, void *stream);
 
 /* Host helper: srand(seed) then n draws of (float)rand()/(float)RAND_MAX
  * (gpt2 != 0: (float)(rand()%1000000)/1000000.0f), the reference's RNG

@@ -77,6 +77,7 @@ EXPORTS = [
     ("lal_gpu_quantize_x", _i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     ("lal_gpu_lm_head_q8", _i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
     ("lal_gpu_q8_packed_bytes", _sz, [_i, _i]),
+    ("lal_gpu_lm_head_rerank", _i, [_vp, _vp, _i, _i, _vp, _vp, _i, _i, _vp, _i, _vp]),
     ("lal_gpu_quantize_w_q8", _i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp]),
     ("lal_gpq8_open", _i, [C.c_char_p, C.POINTER(_vp)]),
     ("lal_gpq8_close", None, [_vp]),

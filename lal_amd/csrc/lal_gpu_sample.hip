@@ -2738,6 +2738,121 @@ __global__ __launch_bounds__(256) void lm_head_scalar_kernel(const int8_t *xq, c
 }
 
 // ---------------------------------------------------------------------------
+// GPT-2 LM head, pass 2 (tools/server/gpt2_server.c:2155-2215): the R largest
+// int8 logits of a row are re-scored in fp32.  The set is the one the
+// reference's min-heap of R (index order, a value enters when the heap has
+// room or it exceeds the root) keeps.  It is every value >= the R-th largest
+// T (with multiplicity) unless values equal to T straddle the boundary: then
+// which of them stay depends on the heap's history, and wave 0 replays the
+// heap (a wave filters each 64 values against the root, one lane applies the
+// pushes and root replacements in order).
+// ---------------------------------------------------------------------------
+constexpr int RERANK_MAX = 512;
+constexpr int RERANK_MAXN = 8192;  // hidden size staged in LDS
+
+struct RerankSmem {
+    float x[RERANK_MAXN];
+    float hv[RERANK_MAX];
+    int hi[RERANK_MAX];
+    int size;
+};
+
+__global__ __launch_bounds__(256) void rerank_rows_kernel(const float *xs, int n, const int8_t *wq, const float *ws,
+                                                          int V, int R, float *logits, int ld, const int *sel_ids,
+                                                          const int *sel_n)
+{
+    __shared__ RerankSmem S;
+    const int b = blockIdx.x, tid = threadIdx.x, lane = lane_id();
+    const float *xr = xs + (size_t)b * n;
+    for (int i = tid; i < n; i += 256) S.x[i] = xr[i];
+    const int r_eff = min(R, V);
+    float *row = logits + (size_t)b * ld;
+    const bool replay = sel_n[b] != r_eff;  // values equal to T straddle the boundary
+    if (replay && wave_id() == 0) {
+        // the reference heap (gpt2_server.c:2165-2192), replayed in index
+        // order: in each chunk of 64, the first value that acts on the
+        // current heap (any while it fills, then above the root) is applied
+        // by lane 0; values before it cannot act, as the heap is unchanged
+        int size = 0;
+        for (int base = 0; base < V; base += 64) {
+            const int v = base + lane;
+            const float x = (v < V) ? row[v] : 0.0f;
+            unsigned long long todo = __ballot(v < V);
+            while (todo) {
+                const float root = (size < R) ? -INFINITY : S.hv[0];
+                const unsigned long long m = __ballot(size < R || x > root) & todo;
+                if (!m) break;
+                const int l = (int)__builtin_ctzll(m);
+                const float xv = readlane_f(x, l);
+                if (lane == 0) {
+                    if (size < R) {
+                        int c = size;
+                        S.hv[c] = xv;
+                        S.hi[c] = base + l;
+                        while (c > 0) {
+                            const int pp = (c - 1) >> 1;
+                            if (S.hv[pp] <= S.hv[c]) break;
+                            const float tv = S.hv[pp]; S.hv[pp] = S.hv[c]; S.hv[c] = tv;
+                            const int ti = S.hi[pp]; S.hi[pp] = S.hi[c]; S.hi[c] = ti;
+                            c = pp;
+                        }
+                    } else {
+                        S.hv[0] = xv;
+                        S.hi[0] = base + l;
+                        int pp = 0;
+                        for (;;) {
+                            const int lc = 2 * pp + 1, rc = 2 * pp + 2;
+                            int sm = pp;
+                            if (lc < size && S.hv[lc] < S.hv[sm]) sm = lc;
+                            if (rc < size && S.hv[rc] < S.hv[sm]) sm = rc;
+                            if (sm == pp) break;
+                            const float tv = S.hv[pp]; S.hv[pp] = S.hv[sm]; S.hv[sm] = tv;
+                            const int ti = S.hi[pp]; S.hi[pp] = S.hi[sm]; S.hi[sm] = ti;
+                            pp = sm;
+                        }
+                    }
+                }
+                if (size < R) ++size;
+                wave_sync();
+                todo &= (l == 63) ? 0ull : (~0ull << (l + 1));
+            }
+        }
+    }
+    __syncthreads();
+    // fp32 re-score (gpt2_server.c:2200-2213): w_row[i] = wq[i] * scale, eight
+    // fused multiply-add lanes over i mod 8, their sum in lane order, then
+    // the tail one fused multiply-add at a time
+    const int *ids = sel_ids + (size_t)b * R;
+    const bool vec8 = ((n & 7) == 0) && ((((uintptr_t)wq) & 7) == 0);
+    for (int j = tid; j < r_eff; j += 256) {
+        const int v = replay ? S.hi[j] : ids[j];
+        const int8_t *w = wq + (size_t)v * n;
+        const float sc = ws[v];
+        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
+        int i = 0;
+        if (vec8) {
+            for (; i + 8 <= n; i += 8) {
+                const uint2 q = *reinterpret_cast<const uint2 *>(w + i);
+#pragma unroll
+                for (int c = 0; c < 8; ++c) {
+                    const int8_t qb = (int8_t)(((c < 4 ? q.x : q.y) >> (8 * (c & 3))) & 0xFFu);
+                    acc[c] = fmaf(S.x[i + c], (float)qb * sc, acc[c]);
+                }
+            }
+        } else {
+            for (; i + 8 <= n; i += 8)
+#pragma unroll
+                for (int c = 0; c < 8; ++c) acc[c] = fmaf(S.x[i + c], (float)w[i + c] * sc, acc[c]);
+        }
+        float sum = acc[0];
+#pragma unroll
+        for (int c = 1; c < 8; ++c) sum = sum + acc[c];
+        for (; i < n; ++i) sum = fmaf(S.x[i], (float)w[i] * sc, sum);
+        row[v] = sum;
+    }
+}
+
+// ---------------------------------------------------------------------------
 // synthetic workloads (benchmarks / tests)
 // ---------------------------------------------------------------------------
 __device__ __forceinline__ uint64_t mix64(uint64_t z)
@@ -2884,6 +2999,12 @@ struct lal_gpu_ctx {
     int *lst_idx;
     int4 *lst_meta;
     unsigned *arrive;
+    // LM head re-rank (lal_gpu_lm_head_rerank): the selected ids per row, the
+    // selection's pool size, zero uniforms and a token sink for the selection
+    int *rr_ids;
+    int *rr_n;
+    float *rr_u;
+    int *rr_tok;
 };
 
 static thread_local hipError_t g_last_hip = hipSuccess;
@@ -2956,6 +3077,11 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     if (e == hipSuccess) e = hipMalloc((void **)&c->lst_meta, (size_t)max_batch * MAX_SLICES * sizeof(int4));
     if (e == hipSuccess) e = hipMalloc((void **)&c->arrive, (size_t)max_batch * sizeof(unsigned));
     if (e == hipSuccess) e = hipMemset(c->arrive, 0, (size_t)max_batch * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->rr_ids, (size_t)max_batch * RERANK_MAX * sizeof(int));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->rr_n, (size_t)max_batch * sizeof(int));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->rr_u, (size_t)max_batch * sizeof(float));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->rr_tok, (size_t)max_batch * sizeof(int));
+    if (e == hipSuccess) e = hipMemset(c->rr_u, 0, (size_t)max_batch * sizeof(float));
     if (e != hipSuccess) {
         lal_gpu_destroy(c);
         return e == hipErrorOutOfMemory ? LAL_GPU_E_NOMEM : hip_fail(e);
@@ -2973,6 +3099,10 @@ void lal_gpu_destroy(lal_gpu_ctx *ctx)
     if (ctx->lst_idx) (void)hipFree(ctx->lst_idx);
     if (ctx->lst_meta) (void)hipFree(ctx->lst_meta);
     if (ctx->arrive) (void)hipFree(ctx->arrive);
+    if (ctx->rr_ids) (void)hipFree(ctx->rr_ids);
+    if (ctx->rr_n) (void)hipFree(ctx->rr_n);
+    if (ctx->rr_u) (void)hipFree(ctx->rr_u);
+    if (ctx->rr_tok) (void)hipFree(ctx->rr_tok);
     if (cur >= 0 && cur != ctx->device) (void)hipSetDevice(cur);
     free(ctx);
 }
@@ -3248,6 +3378,39 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
         }
         LAL_HIP(hipGetLastError());
     }
+    return LAL_GPU_OK;
+}
+
+int lal_gpu_lm_head_rerank(lal_gpu_ctx *ctx, const float *d_x, int batch, int n, const int8_t *d_wq,
+                           const float *d_ws, int vocab, int rerank_n, float *d_logits, int ld, void *stream)
+{
+    if (!ctx || !d_x || !d_wq || !d_ws || !d_logits) return LAL_GPU_E_INVAL;
+    if (batch <= 0 || n <= 0 || vocab <= 0 || rerank_n <= 0 || ld < vocab) return LAL_GPU_E_INVAL;
+    if (batch > ctx->max_batch || vocab > ctx->max_vocab || rerank_n > RERANK_MAX || n > RERANK_MAXN)
+        return LAL_GPU_E_RANGE;
+    // the R largest pass-1 logits with multiplicity, through the sampler's
+    // selection (no penalty, ids ascending); the pool size tells whether ties
+    // straddle the boundary
+    lal_gpu_sample_params p;
+    memset(&p, 0, sizeof p);
+    p.temperature = 1.0f;
+    p.top_k = rerank_n;
+    p.rep_penalty = 1.0f;
+    p.variant = LAL_GPU_VARIANT_BASIC;
+    lal_gpu_sample_io io;
+    memset(&io, 0, sizeof io);
+    io.logits = d_logits;
+    io.ld = ld;
+    io.uniforms = ctx->rr_u;
+    io.out_token = ctx->rr_tok;
+    io.out_n_cand = ctx->rr_n;
+    io.cand_ld = rerank_n;
+    io.cand_ids = ctx->rr_ids;
+    int rc = lal_gpu_sample(ctx, batch, vocab, &p, &io, stream);
+    if (rc != LAL_GPU_OK) return rc;
+    hipLaunchKernelGGL(rerank_rows_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, d_x, n, d_wq, d_ws, vocab,
+                       rerank_n, d_logits, ld, (const int *)ctx->rr_ids, (const int *)ctx->rr_n);
+    LAL_HIP(hipGetLastError());
     return LAL_GPU_OK;
 }
 

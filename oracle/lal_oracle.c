@@ -410,6 +410,65 @@ void lal_oracle_quantize_w(const float *W, int8_t *q, float *scale,
     }
 }
 
+/* gpt2_server.c:2155-2192: min-heap of (value, id), root = smallest kept;
+ * a value enters while there is room, later only when it exceeds the root. */
+int lal_oracle_gpt2_rerank(float *logits, const float *x, const int8_t *wq,
+                           const float *ws, int V, int n, int R, int *ids)
+{
+    float *hv = (float *)malloc((size_t)R * sizeof(float));
+    int *hi = (int *)malloc((size_t)R * sizeof(int));
+    int size = 0;
+    for (int v = 0; v < V; v++) {
+        const float val = logits[v];
+        if (size < R) {
+            int c = size++;
+            hv[c] = val;
+            hi[c] = v;
+            while (c > 0) {
+                const int up = (c - 1) >> 1;
+                if (hv[up] <= hv[c]) break;
+                float t = hv[up]; hv[up] = hv[c]; hv[c] = t;
+                int ti = hi[up]; hi[up] = hi[c]; hi[c] = ti;
+                c = up;
+            }
+        } else if (val > hv[0]) {
+            hv[0] = val;
+            hi[0] = v;
+            int at = 0;
+            for (;;) {
+                const int a = 2 * at + 1, b = a + 1;
+                int lo = at;
+                if (a < size && hv[a] < hv[lo]) lo = a;
+                if (b < size && hv[b] < hv[lo]) lo = b;
+                if (lo == at) break;
+                float t = hv[at]; hv[at] = hv[lo]; hv[lo] = t;
+                int ti = hi[at]; hi[at] = hi[lo]; hi[lo] = ti;
+                at = lo;
+            }
+        }
+    }
+    /* gpt2_server.c:2200-2213 */
+    float *w = (float *)malloc((size_t)n * sizeof(float));
+    for (int j = 0; j < size; j++) {
+        const int v = hi[j];
+        const float sc = ws[v];
+        for (int i = 0; i < n; i++) w[i] = (float)wq[(size_t)v * n + i] * sc;
+        float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        int i = 0;
+        for (; i + 8 <= n; i += 8)
+            for (int c = 0; c < 8; c++) lane[c] = fmaf(x[i + c], w[i + c], lane[c]);
+        float s = lane[0];
+        for (int c = 1; c < 8; c++) s = s + lane[c];
+        for (; i < n; i++) s = fmaf(x[i], w[i], s);
+        logits[v] = s;
+        if (ids) ids[j] = v;
+    }
+    free(w);
+    free(hv);
+    free(hi);
+    return size;
+}
+
 /* Filter plugins with the lal_filter_topk ABI (compiler/lal.py:2205-2242):
  * each ban clears a still-kept id and counts it.  antirepeat4 is what
  * demos/mini_antirepeat.lal declares (ban_last; ban_repeat(4)); norepeat6 is

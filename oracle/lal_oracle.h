@@ -124,6 +124,15 @@ void lal_oracle_lm_head(float *logits, const int8_t *xq, float sx,
 void lal_oracle_quantize_w(const float *W, int8_t *q, float *scale,
                            int in_dim, int out_dim);
 
+/* gpt2_server.c:2155-2215: the reference min-heap of R over logits[0..V)
+ * (pass-1 int8 logits), then each kept id re-scored in fp32 from x[n] and
+ * the int8 row wq[v] * ws[v] (eight fused multiply-add lanes over i mod 8,
+ * summed in lane order; the tail with fused multiply-adds).  Updates logits
+ * in place; ids (R entries, or NULL) receive the kept ids in heap order.
+ * Returns the number kept (min(R, V)). */
+int lal_oracle_gpt2_rerank(float *logits, const float *x, const int8_t *wq,
+                           const float *ws, int V, int n, int R, int *ids);
+
 typedef struct { int tokens[256]; int n; } lal_oracle_recent;
 void lal_oracle_recent_push(lal_oracle_recent *rt, int tok);
 

@@ -77,6 +77,8 @@ class Oracle:
         L.lal_oracle_kth_largest_sorted.argtypes = [_fp, C.c_int, C.c_int]
         L.lal_oracle_recent_push.argtypes = [C.c_void_p, C.c_int]
         L.lal_oracle_expf_checksums.argtypes = [C.c_uint, C.c_int, C.POINTER(C.c_uint64)]
+        L.lal_oracle_gpt2_rerank.restype = C.c_int
+        L.lal_oracle_gpt2_rerank.argtypes = [_fp, _fp, C.POINTER(C.c_int8), _fp, C.c_int, C.c_int, C.c_int, _ip]
         self.filter_antirepeat4 = C.cast(L.lal_oracle_filter_antirepeat4, C.c_void_p).value
         self.filter_norepeat6 = C.cast(L.lal_oracle_filter_norepeat6, C.c_void_p).value
         self.filter_fn = {"antirepeat4": self.filter_antirepeat4,
@@ -149,6 +151,14 @@ class Oracle:
         self.L.lal_oracle_quantize_w(_ptr(W, _fp), _ptr(q, C.POINTER(C.c_int8)), _ptr(s, _fp), n, V)
         return q, s
 
+    def gpt2_rerank(self, logits, x, wq, ws, R=512):
+        """In place on `logits` (pass-1 values); returns the kept ids (heap order)."""
+        V, n = wq.shape
+        ids = np.zeros(R, np.int32)
+        k = self.L.lal_oracle_gpt2_rerank(_ptr(logits, _fp), _ptr(x, _fp), _ptr(wq, C.POINTER(C.c_int8)),
+                                          _ptr(ws, _fp), V, n, R, _ptr(ids, _ip))
+        return ids[:k]
+
     def expf_checksums(self, first_hi, nhi):
         out = np.zeros(nhi, np.uint64)
         self.L.lal_oracle_expf_checksums(first_hi, nhi, out.ctypes.data_as(C.POINTER(C.c_uint64)))
@@ -177,6 +187,11 @@ class Reference:
             f.argtypes = [_fp, C.c_int, C.c_float, C.c_int, C.c_float, _ip, C.c_int]
         L.lal_ref_set_filter.argtypes = [C.c_void_p]
         L.lal_ref_vocab_capacity.restype = C.c_int
+        L.lal_ref_gpt2_vocab.restype = C.c_int
+        L.lal_ref_gpt2_embd.restype = C.c_int
+        L.lal_ref_gpt2_lm_head.argtypes = [_fp, _fp, C.POINTER(C.c_int8), _fp]
+        L.lal_ref_gpt2_quantize_row.restype = C.c_float
+        L.lal_ref_gpt2_quantize_row.argtypes = [_fp, C.POINTER(C.c_int8), C.c_int]
         L.lal_ref_recent_push.argtypes = [_ip, _ip, C.c_int]
         for sfx in ("avx2", "scalar"):
             f = getattr(L, f"lal_ref_quantize_x_int8_{sfx}")
@@ -188,6 +203,18 @@ class Reference:
                               C.c_int, C.c_int, C.c_int]
             q = getattr(L, f"lal_ref_quantize_q8_per_row_{sfx}")
             q.argtypes = [_fp, C.POINTER(C.c_int8), _fp, C.c_int, C.c_int]
+
+    def gpt2_lm_head(self, x, wq, ws):
+        """gpt2_server.c's lm_head_int8_parallel at its own shapes."""
+        V = self.L.lal_ref_gpt2_vocab()
+        out = np.zeros(V, np.float32)
+        self.L.lal_ref_gpt2_lm_head(_ptr(out, _fp), _ptr(x, _fp), _ptr(wq, C.POINTER(C.c_int8)), _ptr(ws, _fp))
+        return out
+
+    def gpt2_quantize_row(self, x):
+        q = np.zeros(len(x), np.int8)
+        s = self.L.lal_ref_gpt2_quantize_row(_ptr(x, _fp), _ptr(q, C.POINTER(C.c_int8)), len(x))
+        return np.float32(s), q
 
     def sample(self, row, V, T, k, pen, hist, seed, filtered=False, filt=None):
         h = None if hist is None else np.ascontiguousarray(hist, np.int32)

@@ -234,3 +234,53 @@ def test_top_p_draw_endpoints():
         # gpt2 draw convention: r == 0 returns id 0 whether or not it is kept
         pg = make_params(temperature=0.8, top_k=100, top_p=0.7, flags=0x2)
         assert ORC.sample_row(row.copy(), pg, u=0.0)[0] == 0
+
+
+def _gpt2_case(seed, V, n, tie_rows=0, strong_rows=0):
+    """wte ~ N(0, 0.1) quantized per row by truncation (gpt2_server.c:3752-3761),
+    hidden x ~ N(0, 1).  tie_rows copies of one strong row (scaled 0.93) give
+    equal int8 logits straddling the 512th place; strong_rows copies scaled
+    0.97, spread through the vocabulary, evict some of them from the heap, so
+    that which ties stay depends on the heap's history."""
+    rng = np.random.default_rng(seed)
+    wte = (rng.standard_normal((V, n)) * 0.1).astype(np.float32)
+    x = rng.standard_normal(n).astype(np.float32)
+    if tie_rows:
+        base = wte[int(np.argmax(wte @ x))].copy()
+        idx = rng.choice(V, tie_rows + strong_rows, replace=False)
+        wte[idx[:tie_rows]] = base * np.float32(0.93)
+        wte[idx[tie_rows:]] = base * np.float32(0.97)
+    wq = np.zeros((V, n), np.int8)
+    ws = np.zeros(V, np.float32)
+    for v in range(V):
+        s, q = ORC.quantize_x(wte[v].copy(), 1)
+        ws[v], wq[v] = s, q
+    return x, wq, ws
+
+
+@pytest.mark.parametrize("seed,ties,strong", [(1, 0, 0), (2, 0, 0), (3, 600, 100), (10, 520, 40)])
+def test_gpt2_rerank_against_reference(ref, seed, ties, strong):
+    """The oracle's int8-select + fp32 re-rank (pass 1 through the oracle's
+    quantizer and LM head, pass 2 through lal_oracle_gpt2_rerank) equals the
+    reference's lm_head_int8_parallel bit for bit at the server's shapes,
+    including boundary ties resolved by the heap's history (cases where
+    neither the first nor the last ties by index are the ones kept)."""
+    V, n = ref.L.lal_ref_gpt2_vocab(), ref.L.lal_ref_gpt2_embd()
+    x, wq, ws = _gpt2_case(seed, V, n, ties, strong)
+    want = ref.gpt2_lm_head(x, wq, ws)
+    sx, xq = ORC.quantize_x(x.copy(), 1)
+    s_ref, q_ref = ref.gpt2_quantize_row(x.copy())
+    assert s_ref.view(np.uint32) == sx.view(np.uint32) and np.array_equal(q_ref, xq)
+    p1 = ORC.lm_head(xq, sx, wq, ws)
+    got = p1.copy()
+    ids = ORC.gpt2_rerank(got, x, wq, ws)
+    assert len(ids) == 512
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    if ties:
+        T = np.sort(p1)[::-1][511]
+        above = set(np.nonzero(p1 > T)[0].tolist())
+        eq = np.nonzero(p1 == T)[0].tolist()
+        r = 512 - len(above)
+        assert 0 < r < len(eq), "ties straddle the boundary"
+        kept = set(ids.tolist())
+        assert kept != above | set(eq[:r]) and kept != above | set(eq[-r:])
