@@ -45,6 +45,16 @@ for _b in (1, 16, 64):
                                                 top_p=0.0, pen=1.1, H=64)
 
 
+# GPT-2 LM head with fp32 re-rank + sampling (tools/server/gpt2_server.c:2125-2215,
+# 2862-3012): wte [50257, 768] ~ N(0, 0.1) quantized per row by truncation at
+# set-up, hidden [B, 768] ~ N(0, 1); a step is quantize + int8 LM head +
+# re-rank of the top 512 in fp32 + sampling (T 1.0, top-k 40, penalty 1.2 over
+# 128 ids, the GPT-2 draw and uniforms).
+for _b in (1, 16):
+    WORKLOADS[f"gpt2_lm_head_rerank_b{_b}"] = dict(B=_b, V=50257, kind="gpt2lm", n=768, T=1.0, k=40,
+                                                   top_p=0.0, pen=1.2, H=128, gpt2=True, rerank=512)
+
+
 def lm_head_weight_bytes(w):
     return w["V"] * w["n"] + 4 * w["V"]
 
@@ -60,8 +70,9 @@ def algorithmic_bytes_per_row(w):
 
 
 def algorithmic_bytes_per_step(w):
-    if w["kind"] == "lmhead":
+    if w["kind"] in ("lmhead", "gpt2lm"):
         # W and its scales once, each row's hidden state and history, the id
+        # (the re-rank's 512 rows per row come from cache-resident W)
         return lm_head_weight_bytes(w) + w["B"] * (4 * w["n"] + 4 * w["H"] + 4 + 4)
     b = w["B"] * algorithmic_bytes_per_row(w)
     if w.get("bias_nnz"):
@@ -93,6 +104,20 @@ class Inputs:
                 L["wpk"] = dev.alloc(lib.lal_gpu_q8_packed_bytes(V, n))
                 abi.check(lib.lal_gpu_pack_q8(dev.ctx, abi.ptr(L["w"]), V, n, abi.ptr(L["wpk"]), dev.stream),
                           "pack")
+        elif w["kind"] == "gpt2lm":
+            n = w["n"]
+            self.lmhead = dict(n=n, w=dev.alloc(V * n), sw=dev.alloc(4 * V), x=dev.alloc(4 * B * n),
+                               xq=dev.alloc(B * n), sx=dev.alloc(4 * B), wpk=None, gpt2=True)
+            L = self.lmhead
+            wte = dev.alloc(4 * V * n)
+            abi.check(lib.lal_gpu_synth_normal(abi.ptr(wte), V * n, seed + 5, C.c_float(0.1), dev.stream), "wte")
+            # load-time quantization of the wte rows (gpt2_server.c:3752-3761)
+            abi.check(lib.lal_gpu_quantize_x(dev.ctx, abi.ptr(wte), V, n, 1, abi.ptr(L["w"]), abi.ptr(L["sw"]),
+                                             dev.stream), "quantize wte")
+            abi.check(lib.lal_gpu_synth_normal(abi.ptr(L["x"]), B * n, seed + 7, C.c_float(1.0), dev.stream),
+                      "x")
+            dev.sync()
+            wte.close()
         elif w["kind"] == "zipf":
             abi.check(lib.lal_gpu_synth_zipf(abi.ptr(self.logits), B, V, V, seed, C.c_float(1.1),
                                              C.c_float(0.3), dev.stream), "synth")
@@ -105,7 +130,8 @@ class Inputs:
         self.hist = dev.alloc(4 * B * H)
         abi.check(lib.lal_gpu_synth_ids(abi.ptr(self.hist), B * H, seed + 1, V, dev.stream), "ids")
         u = np.zeros(B, np.float32)
-        lib.lal_gpu_uniforms_rand(seed & 0xFFFFFFFF, B, u.ctypes.data_as(C.POINTER(C.c_float)), 0)
+        lib.lal_gpu_uniforms_rand(seed & 0xFFFFFFFF, B, u.ctypes.data_as(C.POINTER(C.c_float)),
+                                  1 if w.get("gpt2") else 0)
         self.u = dev.put(u)
         self.allow = None
         self.words = (V + 31) // 32
@@ -143,7 +169,8 @@ class Inputs:
 def params_for(w):
     from lal_amd import abi
     return abi.make_params(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"],
-                           variant=abi.VARIANT_BASIC, mask_recent=w.get("mask_recent", 0))
+                           variant=abi.VARIANT_BASIC, mask_recent=w.get("mask_recent", 0),
+                           flags=abi.F_DRAW_GPT2 if w.get("gpt2") else 0)
 
 
 def cpu_baseline(w, dev, inputs, target_s=4.0):
@@ -206,17 +233,23 @@ def cpu_baseline_lmhead(w, dev, inputs):
     p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"])
     threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
     done, t0 = 0, time.perf_counter()
+    gpt2 = bool(w.get("gpt2"))
+    if gpt2:
+        p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"], flags=2)
     while True:
-        sx, xq = orc.quantize_x(x, 0)
-        logits = orc.lm_head(xq, sx, W, sw, nthreads=threads)[None, :]
-        orc.sample_batch(logits, p, hist=h, uniforms=u, nthreads=1)
+        sx, xq = orc.quantize_x(x, 1 if gpt2 else 0)
+        logits = orc.lm_head(xq, sx, W, sw, nthreads=threads)
+        if gpt2:
+            orc.gpt2_rerank(logits, x, W, sw, w["rerank"])
+        orc.sample_batch(logits[None, :], p, hist=h, uniforms=u, nthreads=1)
         done += 1
         el = time.perf_counter() - t0
         if el >= 4.0 or done >= 32:
             break
     return {"value": done / el, "unit": "rows/s", "cores": threads, "kind": "port",
             "sample": f"{done} rows (row 0 of the batch, repeated): quantize, LM head over "
-                      f"{V} x {n} int8 with OpenMP over vocab rows, sampler"}
+                      f"{V} x {n} int8 with OpenMP over vocab rows, "
+                      f"{'re-rank of the top 512, ' if gpt2 else ''}sampler"}
 
 
 def read_traffic(name):
@@ -256,7 +289,7 @@ def main():
     from lal_amd import abi
     w = WORKLOADS[args.workload]
     dev = abi.Device(0, max_batch=w["B"], max_vocab=w["V"])
-    nsets = 1 if w["kind"] == "lmhead" else max(1, args.sets)  # W alone exceeds the 256 MB cache
+    nsets = 1 if w["kind"] in ("lmhead", "gpt2lm") else max(1, args.sets)  # W dominates the footprint
     sets = [Inputs(dev, w, 1000 + 17 * i, packed=args.lm_head_layout == "packed") for i in range(nsets)]
     ios = [s.io(w) for s in sets]
     params = params_for(w)
@@ -265,7 +298,8 @@ def main():
         inp = sets[i % len(sets)]
         if inp.lmhead is not None:
             L = inp.lmhead
-            abi.check(dev.lib.lal_gpu_quantize_x(dev.ctx, abi.ptr(L["x"]), w["B"], L["n"], 0, abi.ptr(L["xq"]),
+            abi.check(dev.lib.lal_gpu_quantize_x(dev.ctx, abi.ptr(L["x"]), w["B"], L["n"],
+                                                 1 if L.get("gpt2") else 0, abi.ptr(L["xq"]),
                                                  abi.ptr(L["sx"]), dev.stream), "quantize_x")
             if L["wpk"] is not None:
                 abi.check(dev.lib.lal_gpu_lm_head_q8_packed(dev.ctx, abi.ptr(L["xq"]), abi.ptr(L["sx"]), w["B"],
@@ -276,6 +310,10 @@ def main():
                 abi.check(dev.lib.lal_gpu_lm_head_q8(dev.ctx, abi.ptr(L["xq"]), abi.ptr(L["sx"]), w["B"], L["n"],
                                                      abi.ptr(L["w"]), abi.ptr(L["sw"]), w["V"],
                                                      abi.ptr(inp.logits), w["V"], dev.stream), "lm_head_q8")
+            if L.get("gpt2"):
+                abi.check(dev.lib.lal_gpu_lm_head_rerank(dev.ctx, abi.ptr(L["x"]), w["B"], L["n"], abi.ptr(L["w"]),
+                                                         abi.ptr(L["sw"]), w["V"], w["rerank"],
+                                                         abi.ptr(inp.logits), w["V"], dev.stream), "rerank")
         dev.sample(w["B"], w["V"], params, ios[i % len(ios)])
 
     for i in range(args.warmup):
@@ -316,6 +354,8 @@ def main():
                    "top_p": w["top_p"], "rep_penalty": w["pen"], "history_ids": w["H"],
                    **({"hidden": w["n"], "lm_head": "int8 [152064, 3584] + per-row fp32 scales"}
                       if w["kind"] == "lmhead" else {}),
+                   **({"hidden": w["n"], "lm_head": "int8 [50257, 768] + per-row fp32 scales, top 512 "
+                       "re-scored in fp32", "draw": "gpt2"} if w["kind"] == "gpt2lm" else {}),
                    "rotating_input_sets": len(sets),
                    "live_input_bytes": len(sets) * 4 * w["B"] * w["V"],
                    **({"allow_p": w["allow"], "bias_nnz": w["bias_nnz"],
@@ -327,7 +367,7 @@ def main():
         "wall_s_timed_region": wall,
     }
     if not args.no_cpu_baseline:
-        if w["kind"] == "lmhead":
+        if w["kind"] in ("lmhead", "gpt2lm"):
             out["cpu_baseline"] = cpu_baseline_lmhead(w, dev, sets[0])
         else:
             out["cpu_baseline"] = cpu_baseline(w, dev, sets[0])

@@ -2746,29 +2746,208 @@ __global__ __launch_bounds__(256) void lm_head_scalar_kernel(const int8_t *xq, c
 // which of them stay depends on the heap's history, and wave 0 replays the
 // heap (a wave filters each 64 values against the root, one lane applies the
 // pushes and root replacements in order).
+// One workgroup of 1024 threads per row; the row (at most RR_VPT * 1024
+// values) is held in registers, T is found bit by bit with block-wide counts
+// from the highest bit where the row's largest and smallest keys differ.
 // ---------------------------------------------------------------------------
 constexpr int RERANK_MAX = 512;
 constexpr int RERANK_MAXN = 8192;  // hidden size staged in LDS
+constexpr int RR_WG = 1024;
+constexpr int RR_WAVES = RR_WG / 64;
+constexpr int RR_VPT = 64;         // row values per thread: vocab <= 65536
+
+constexpr int RR_CAP = 1024;       // gathered keys for the exact search
 
 struct RerankSmem {
-    float x[RERANK_MAXN];
     float hv[RERANK_MAX];
     int hi[RERANK_MAX];
-    int size;
+    int red[2][RR_WAVES];
+    unsigned redk[2][RR_WAVES];
+    unsigned gk[RR_WG > RR_CAP ? RR_WG : RR_CAP];  // threads' largest keys, then the gathered keys
+    int gi[RR_CAP];       // ... and their ids
+    unsigned bound;
+    int flag;
 };
 
-__global__ __launch_bounds__(256) void rerank_rows_kernel(const float *xs, int n, const int8_t *wq, const float *ws,
-                                                          int V, int R, float *logits, int ld, const int *sel_ids,
-                                                          const int *sel_n)
+__device__ __forceinline__ int rr_block_sum(RerankSmem &S, int v, int slot)
+{
+    v = wave_sum(v);
+    if (lane_id() == 0) S.red[slot][wave_id()] = v;
+    __syncthreads();
+    int t = 0;
+#pragma unroll
+    for (int w = 0; w < RR_WAVES; ++w) t += S.red[slot][w];
+    return t;
+}
+
+// k-th largest of the keys q[0..NQ) held by one wave's lanes (0 = none), bit
+// by bit from the top bit where lo and hi differ (lo <= every candidate <= hi):
+// the largest K with at least k keys >= K.  Per-lane counts summed across the
+// wave; wave-synchronous.
+template <int NQ>
+__device__ __forceinline__ uint32_t rr_wave_kth(const uint32_t (&q)[NQ], int k, uint32_t lo, uint32_t hi)
+{
+    if (lo >= hi) return hi;
+    const int top = 31 - __builtin_clz(lo ^ hi);
+    uint32_t K = (top == 31) ? 0u : (hi & ~((2u << top) - 1u));
+    for (int bit = top; bit >= 0; --bit) {
+        const uint32_t cand = K | (1u << bit);
+        // per-lane count as a pairwise tree (short dependency chains)
+        int t[NQ];
+#pragma unroll
+        for (int i = 0; i < NQ; ++i) t[i] = (q[i] >= cand) ? 1 : 0;
+#pragma unroll
+        for (int h = 1; h < NQ; h *= 2)
+#pragma unroll
+            for (int i = 0; i + h < NQ; i += 2 * h) t[i] += t[i + h];
+        if (wave_sum(t[0]) >= k) K = cand;
+    }
+    return K;
+}
+
+__global__ __launch_bounds__(RR_WG) void rerank_select_kernel(int V, int R, const float *logits, int ld, int *out_ids)
 {
     __shared__ RerankSmem S;
-    const int b = blockIdx.x, tid = threadIdx.x, lane = lane_id();
-    const float *xr = xs + (size_t)b * n;
-    for (int i = tid; i < n; i += 256) S.x[i] = xr[i];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = lane_id(), w = wave_id();
+    const float *row = logits + (size_t)b * ld;
     const int r_eff = min(R, V);
-    float *row = logits + (size_t)b * ld;
-    const bool replay = sel_n[b] != r_eff;  // values equal to T straddle the boundary
-    if (replay && wave_id() == 0) {
+    // the row's keys (0 = past the row)
+    uint32_t key[RR_VPT];
+    uint32_t kx = 0u, kn = 0xFFFFFFFFu;
+    float val[RR_VPT];
+#pragma unroll
+    for (int j = 0; j < RR_VPT; ++j) val[j] = row[min(tid + RR_WG * j, V - 1)];  // one burst of loads
+#pragma unroll
+    for (int j = 0; j < RR_VPT; ++j) {
+        const bool in = tid + RR_WG * j < V;
+        key[j] = in ? fkey(val[j]) : 0u;
+        kx = max(kx, key[j]);
+        kn = min(kn, in ? key[j] : 0xFFFFFFFFu);
+    }
+    S.gk[tid] = kx;  // this thread's largest key
+    kx = wave_max_u(kx);
+    kn = wave_min_u(kn);
+    if (lane == 0) {
+        S.redk[0][w] = kx;
+        S.redk[1][w] = kn;
+    }
+    __syncthreads();
+    kx = 0u;
+    kn = 0xFFFFFFFFu;
+#pragma unroll
+    for (int ww = 0; ww < RR_WAVES; ++ww) {
+        kx = max(kx, S.redk[0][ww]);
+        kn = min(kn, S.redk[1][ww]);
+    }
+    // A lower bound L of T: the r_eff-th largest of the threads' largest keys
+    // (r_eff distinct row values reach it); the keys >= L then hold the pool.
+    if (w == 0) {
+        uint32_t L = 0u;
+        if (V > RR_CAP) {
+            uint32_t q[RR_WG / 64], qx = 0u, qn = 0xFFFFFFFFu;
+#pragma unroll
+            for (int i = 0; i < RR_WG / 64; ++i) {
+                q[i] = S.gk[lane + 64 * i];
+                qx = max(qx, q[i]);
+                qn = min(qn, q[i]);
+            }
+            // every thread holds a row value here (V > RR_CAP >= RR_WG), so
+            // the answer lies within the maxima's own range
+            L = rr_wave_kth<RR_WG / 64>(q, r_eff, wave_min_u(qn), wave_max_u(qx));
+        }
+        if (lane == 0) S.bound = L;
+    }
+    __syncthreads();
+    const uint32_t L = S.bound;
+    int mine = 0;
+#pragma unroll
+    for (int j = 0; j < RR_VPT; ++j) mine += (key[j] >= L && key[j] != 0u) ? 1 : 0;
+    const int incl = wave_incl_scan(mine);
+    if (lane == 63) S.red[0][w] = incl;
+    __syncthreads();
+    int ng = 0, off = incl - mine;
+#pragma unroll
+    for (int ww = 0; ww < RR_WAVES; ++ww) {
+        ng += S.red[0][ww];
+        off += (ww < w) ? S.red[0][ww] : 0;
+    }
+    uint32_t K;
+    bool replay;
+    if (ng >= r_eff && ng <= RR_CAP) {
+        // gather the keys >= L (they hold the top r_eff), exact search by wave 0
+#pragma unroll
+        for (int j = 0; j < RR_VPT; ++j)
+            if (key[j] >= L && key[j] != 0u) {
+                S.gk[off] = key[j];
+                S.gi[off] = tid + RR_WG * j;
+                off++;
+            }
+        __syncthreads();
+        if (w == 0) {
+            uint32_t q[RR_CAP / 64];
+#pragma unroll
+            for (int i = 0; i < RR_CAP / 64; ++i) q[i] = (lane + 64 * i < ng) ? S.gk[lane + 64 * i] : 0u;
+            const uint32_t Kw = rr_wave_kth<RR_CAP / 64>(q, r_eff, max(L, kn), kx);
+            int nge = 0;
+#pragma unroll
+            for (int i = 0; i < RR_CAP / 64; ++i) nge += __popcll(__ballot(q[i] >= Kw && q[i] != 0u));
+            if (lane == 0) {
+                S.bound = Kw;
+                S.flag = (nge != r_eff) ? 1 : 0;  // values equal to T straddle the boundary
+            }
+            if (nge == r_eff) {
+                // every gathered key >= T, compacted in gather order
+                int base = 0;
+#pragma unroll
+                for (int i = 0; i < RR_CAP / 64; ++i) {
+                    const bool p = q[i] >= Kw && q[i] != 0u;
+                    const unsigned long long m = __ballot(p);
+                    if (p) S.hi[base + lanes_below(m)] = S.gi[lane + 64 * i];
+                    base += __popcll(m);
+                }
+            }
+        }
+        __syncthreads();
+        K = S.bound;
+        replay = S.flag != 0;
+    } else {
+        // the bound failed or left too many: search the whole row
+        K = kx;
+        if (kn < kx) {
+            const int top = 31 - __builtin_clz(kn ^ kx);
+            K = (top == 31) ? 0u : (kx & ~((2u << top) - 1u));
+            for (int bit = top, slot = 1; bit >= 0; --bit, slot ^= 1) {
+                const uint32_t cand = K | (1u << bit);
+                int c = 0;
+#pragma unroll
+                for (int j = 0; j < RR_VPT; ++j) c += (key[j] >= cand) ? 1 : 0;
+                if (rr_block_sum(S, c, slot) >= r_eff) K = cand;
+            }
+        }
+        int na = 0, ne = 0;
+#pragma unroll
+        for (int j = 0; j < RR_VPT; ++j) {
+            na += (key[j] > K) ? 1 : 0;
+            ne += (key[j] == K && key[j] != 0u) ? 1 : 0;
+        }
+        __syncthreads();
+        const int n_above = rr_block_sum(S, na, 0);
+        const int n_eq = rr_block_sum(S, ne, 1);
+        replay = n_above + n_eq != r_eff;
+        if (!replay) {
+            int m2 = na + ne;
+            const int inc2 = wave_incl_scan(m2);
+            __syncthreads();
+            if (lane == 63) S.red[0][w] = inc2;
+            __syncthreads();
+            int o2 = inc2 - m2;
+            for (int ww = 0; ww < w; ++ww) o2 += S.red[0][ww];
+#pragma unroll
+            for (int j = 0; j < RR_VPT; ++j)
+                if (key[j] >= K && key[j] != 0u) S.hi[o2++] = tid + RR_WG * j;
+        }
+    }
+    if (replay && w == 0) {
         // the reference heap (gpt2_server.c:2165-2192), replayed in index
         // order: in each chunk of 64, the first value that acts on the
         // current heap (any while it fills, then above the root) is applied
@@ -2819,36 +2998,69 @@ __global__ __launch_bounds__(256) void rerank_rows_kernel(const float *xs, int n
         }
     }
     __syncthreads();
-    // fp32 re-score (gpt2_server.c:2200-2213): w_row[i] = wq[i] * scale, eight
-    // fused multiply-add lanes over i mod 8, their sum in lane order, then
-    // the tail one fused multiply-add at a time
-    const int *ids = sel_ids + (size_t)b * R;
-    const bool vec8 = ((n & 7) == 0) && ((((uintptr_t)wq) & 7) == 0);
-    for (int j = tid; j < r_eff; j += 256) {
-        const int v = replay ? S.hi[j] : ids[j];
-        const int8_t *w = wq + (size_t)v * n;
-        const float sc = ws[v];
-        float acc[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
-        int i = 0;
-        if (vec8) {
-            for (; i + 8 <= n; i += 8) {
-                const uint2 q = *reinterpret_cast<const uint2 *>(w + i);
-#pragma unroll
-                for (int c = 0; c < 8; ++c) {
-                    const int8_t qb = (int8_t)(((c < 4 ? q.x : q.y) >> (8 * (c & 3))) & 0xFFu);
-                    acc[c] = fmaf(S.x[i + c], (float)qb * sc, acc[c]);
-                }
-            }
-        } else {
-            for (; i + 8 <= n; i += 8)
-#pragma unroll
-                for (int c = 0; c < 8; ++c) acc[c] = fmaf(S.x[i + c], (float)w[i + c] * sc, acc[c]);
+    for (int j = tid; j < r_eff; j += RR_WG) out_ids[(size_t)b * R + j] = S.hi[j];
+}
+
+// fp32 re-score (gpt2_server.c:2200-2213) of the kept ids, RR_PER of them per
+// workgroup: their int8 rows are staged in LDS (one load burst), then lane c
+// of a group of 8 runs the fused multiply-add chain over i = c mod 8 of
+// w_row[i] = wq[i] * scale; the group's first lane sums the 8 chains in lane
+// order and adds the tail one fused multiply-add at a time.
+constexpr int RR_SCORE_WG = 512;
+constexpr int RR_PER = RR_SCORE_WG / 8;       // candidates per workgroup
+constexpr int RR_STAGE = 64 * 1024;           // staged row bytes
+__global__ __launch_bounds__(RR_SCORE_WG) void rerank_score_kernel(const float *xs, int n, const int8_t *wq,
+                                                                   const float *ws, int V, int R, float *logits,
+                                                                   int ld, const int *ids)
+{
+    __shared__ float xsh[RERANK_MAXN];
+    __shared__ __align__(16) int8_t rows[RR_STAGE];
+    const int b = blockIdx.x, tid = threadIdx.x, lane = lane_id();
+    const int r_eff = min(R, V);
+    const int rs = (n + 4) & ~3;                        // staged row stride (bank spread)
+    const int per = min(RR_PER, RR_STAGE / rs);         // candidates this workgroup holds
+    const int j0 = blockIdx.y * per;
+    const int cnt = min(per, r_eff - j0);
+    if (cnt <= 0) return;
+    const float *xr = xs + (size_t)b * n;
+    for (int i = tid; i < n; i += RR_SCORE_WG) xsh[i] = xr[i];
+    const int *idr = ids + (size_t)b * R + j0;
+    if ((n & 15) == 0 && (((uintptr_t)wq) & 15) == 0) {
+        const int c16 = n >> 4;
+        for (int t = tid; t < cnt * c16; t += RR_SCORE_WG) {
+            const int g = t / c16, c = t - g * c16;
+            const int4 v4 = *reinterpret_cast<const int4 *>(wq + (size_t)idr[g] * n + 16 * c);
+            int *d = reinterpret_cast<int *>(rows + g * rs + 16 * c);
+            d[0] = v4.x; d[1] = v4.y; d[2] = v4.z; d[3] = v4.w;
         }
-        float sum = acc[0];
+    } else {
+        for (int t = tid; t < cnt * n; t += RR_SCORE_WG) {
+            const int g = t / n, i = t - g * n;
+            rows[g * rs + i] = wq[(size_t)idr[g] * n + i];
+        }
+    }
+    __syncthreads();
+    const int g = tid >> 3, c8 = tid & 7;
+    const int n8 = n & ~7;
+    float acc = 0.0f;
+    float sc = 0.0f;
+    int v = 0;
+    if (g < cnt) {
+        v = idr[g];
+        sc = ws[v];
+        const int8_t *wr = rows + g * rs;
+        for (int i = c8; i < n8; i += 8) acc = fmaf(xsh[i], (float)wr[i] * sc, acc);
+    }
+    float part[8];
 #pragma unroll
-        for (int c = 1; c < 8; ++c) sum = sum + acc[c];
-        for (; i < n; ++i) sum = fmaf(S.x[i], (float)w[i] * sc, sum);
-        row[v] = sum;
+    for (int c = 0; c < 8; ++c) part[c] = __shfl(acc, (lane & ~7) + c, 64);
+    if (g < cnt && c8 == 0) {
+        float sum = part[0];
+#pragma unroll
+        for (int c = 1; c < 8; ++c) sum = sum + part[c];
+        const int8_t *wr = rows + g * rs;
+        for (int i = n8; i < n; ++i) sum = fmaf(xsh[i], (float)wr[i] * sc, sum);
+        logits[(size_t)b * ld + v] = sum;
     }
 }
 
@@ -2999,12 +3211,7 @@ struct lal_gpu_ctx {
     int *lst_idx;
     int4 *lst_meta;
     unsigned *arrive;
-    // LM head re-rank (lal_gpu_lm_head_rerank): the selected ids per row, the
-    // selection's pool size, zero uniforms and a token sink for the selection
-    int *rr_ids;
-    int *rr_n;
-    float *rr_u;
-    int *rr_tok;
+    int *rr_ids;  // [max_batch][RERANK_MAX] ids kept by lal_gpu_lm_head_rerank's selection
 };
 
 static thread_local hipError_t g_last_hip = hipSuccess;
@@ -3078,10 +3285,6 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     if (e == hipSuccess) e = hipMalloc((void **)&c->arrive, (size_t)max_batch * sizeof(unsigned));
     if (e == hipSuccess) e = hipMemset(c->arrive, 0, (size_t)max_batch * sizeof(unsigned));
     if (e == hipSuccess) e = hipMalloc((void **)&c->rr_ids, (size_t)max_batch * RERANK_MAX * sizeof(int));
-    if (e == hipSuccess) e = hipMalloc((void **)&c->rr_n, (size_t)max_batch * sizeof(int));
-    if (e == hipSuccess) e = hipMalloc((void **)&c->rr_u, (size_t)max_batch * sizeof(float));
-    if (e == hipSuccess) e = hipMalloc((void **)&c->rr_tok, (size_t)max_batch * sizeof(int));
-    if (e == hipSuccess) e = hipMemset(c->rr_u, 0, (size_t)max_batch * sizeof(float));
     if (e != hipSuccess) {
         lal_gpu_destroy(c);
         return e == hipErrorOutOfMemory ? LAL_GPU_E_NOMEM : hip_fail(e);
@@ -3100,9 +3303,6 @@ void lal_gpu_destroy(lal_gpu_ctx *ctx)
     if (ctx->lst_meta) (void)hipFree(ctx->lst_meta);
     if (ctx->arrive) (void)hipFree(ctx->arrive);
     if (ctx->rr_ids) (void)hipFree(ctx->rr_ids);
-    if (ctx->rr_n) (void)hipFree(ctx->rr_n);
-    if (ctx->rr_u) (void)hipFree(ctx->rr_u);
-    if (ctx->rr_tok) (void)hipFree(ctx->rr_tok);
     if (cur >= 0 && cur != ctx->device) (void)hipSetDevice(cur);
     free(ctx);
 }
@@ -3386,30 +3586,16 @@ int lal_gpu_lm_head_rerank(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
 {
     if (!ctx || !d_x || !d_wq || !d_ws || !d_logits) return LAL_GPU_E_INVAL;
     if (batch <= 0 || n <= 0 || vocab <= 0 || rerank_n <= 0 || ld < vocab) return LAL_GPU_E_INVAL;
-    if (batch > ctx->max_batch || vocab > ctx->max_vocab || rerank_n > RERANK_MAX || n > RERANK_MAXN)
-        return LAL_GPU_E_RANGE;
-    // the R largest pass-1 logits with multiplicity, through the sampler's
-    // selection (no penalty, ids ascending); the pool size tells whether ties
-    // straddle the boundary
-    lal_gpu_sample_params p;
-    memset(&p, 0, sizeof p);
-    p.temperature = 1.0f;
-    p.top_k = rerank_n;
-    p.rep_penalty = 1.0f;
-    p.variant = LAL_GPU_VARIANT_BASIC;
-    lal_gpu_sample_io io;
-    memset(&io, 0, sizeof io);
-    io.logits = d_logits;
-    io.ld = ld;
-    io.uniforms = ctx->rr_u;
-    io.out_token = ctx->rr_tok;
-    io.out_n_cand = ctx->rr_n;
-    io.cand_ld = rerank_n;
-    io.cand_ids = ctx->rr_ids;
-    int rc = lal_gpu_sample(ctx, batch, vocab, &p, &io, stream);
-    if (rc != LAL_GPU_OK) return rc;
-    hipLaunchKernelGGL(rerank_rows_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, d_x, n, d_wq, d_ws, vocab,
-                       rerank_n, d_logits, ld, (const int *)ctx->rr_ids, (const int *)ctx->rr_n);
+    if (rerank_n > RERANK_MAX || n > RERANK_MAXN || vocab > RR_VPT * RR_WG) return LAL_GPU_E_RANGE;
+    if (batch > ctx->max_batch) return LAL_GPU_E_RANGE;
+    hipStream_t s = (hipStream_t)stream;
+    hipLaunchKernelGGL(rerank_select_kernel, dim3(batch), dim3(RR_WG), 0, s, vocab, rerank_n, d_logits, ld,
+                       ctx->rr_ids);
+    LAL_HIP(hipGetLastError());
+    const int per = std::min(RR_PER, RR_STAGE / ((n + 4) & ~3));
+    const int r_eff = std::min(rerank_n, vocab);
+    hipLaunchKernelGGL(rerank_score_kernel, dim3(batch, (r_eff + per - 1) / per), dim3(RR_SCORE_WG), 0, s, d_x, n,
+                       d_wq, d_ws, vocab, rerank_n, d_logits, ld, (const int *)ctx->rr_ids);
     LAL_HIP(hipGetLastError());
     return LAL_GPU_OK;
 }
