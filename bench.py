@@ -282,7 +282,7 @@ def main():
     if args.gpus != 1 or world != 1:
         print(json.dumps({"error": "this benchmark runs on one GPU only: the sampler is measured "
                           "on one MI355X; rows are independent, so a multi-GPU run would be "
-                          "batch-sharded with no exchange (see DESIGN.md)",
+                          "batch-sharded with no exchange between GPUs",
                           "n_gpus": args.gpus}))
         sys.exit(2)
 
