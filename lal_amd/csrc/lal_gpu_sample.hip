@@ -1848,27 +1848,71 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         }
         float ltau = -INFINITY;
         bool lstrict = false;
-        float Ts = -INFINITY;
-        if (tot_s >= k) {
-            uint32_t kn, kx;
-            block_key_range(S, kn, kx);
-            Ts = keyf(block_kth_union<CAPW>(S, k, kn, kx));
-        }
-        if (strict_s && (tot_s < k || Ts <= tstar_s)) {
-            ltau = tstar_s;
-            lstrict = true;
-        } else if (tot_s >= k) {
-            ltau = Ts;
-        }
         const int cnt_w = S.wcnt[w];
-        int mine = 0;
+        int mine = 0, n_s = 0, off = 0;
+        bool listed = false;
+        if (k <= 64 && !strict_s && tot_s >= k) {
+            // A cheaper cut first: the k-th largest L of the 256 lanes' largest
+            // entries is at most the slice's k-th largest (k distinct entries
+            // reach it), so the entries >= L hold every value that can reach
+            // the row's pool; used when they fit the list.
+            unsigned *lkeys = S.u.h.whist[0];
+            uint32_t lm = 0u;
+            for (int j = lane; j < cnt_w; j += 64) {
+                const float v = bv[j];
+                if (v == v) lm = max(lm, fkey(v));
+            }
+            lkeys[tid] = lm;
+            __syncthreads();
+            if (w == 0) {
+                const uint32_t q0 = lkeys[lane], q1 = lkeys[64 + lane], q2 = lkeys[128 + lane],
+                               q3 = lkeys[192 + lane];
+                uint32_t K = 0u;
+                for (int bit = 31; bit >= 0; --bit) {
+                    const uint32_t cand = K | (1u << bit);
+                    const int c = __popcll(__ballot(q0 >= cand)) + __popcll(__ballot(q1 >= cand)) +
+                                  __popcll(__ballot(q2 >= cand)) + __popcll(__ballot(q3 >= cand));
+                    if (c >= k) K = cand;
+                }
+                if (lane == 0) S.sel_rem = (int)K;
+            }
+            __syncthreads();
+            const uint32_t L = (uint32_t)S.sel_rem;
+            if (L) {
+                const float lf = keyf(L);
 #pragma unroll
-        for (int r = 0; r < PER; ++r) {
-            const int j = lane + 64 * r;
-            mine += (j < cnt_w) && passes(bv[j], ltau, lstrict);
+                for (int r = 0; r < PER; ++r) {
+                    const int j = lane + 64 * r;
+                    mine += (j < cnt_w) && passes(bv[j], lf, false);
+                }
+                off = block_excl_scan(mine, n_s, S.wsum[0]);
+                if (n_s <= A.lcap) {
+                    ltau = lf;
+                    listed = true;
+                }
+            }
         }
-        int n_s = 0;
-        int off = block_excl_scan(mine, n_s, S.wsum[0]);
+        if (!listed) {
+            float Ts = -INFINITY;
+            if (tot_s >= k) {
+                uint32_t kn, kx;
+                block_key_range(S, kn, kx);
+                Ts = keyf(block_kth_union<CAPW>(S, k, kn, kx));
+            }
+            if (strict_s && (tot_s < k || Ts <= tstar_s)) {
+                ltau = tstar_s;
+                lstrict = true;
+            } else if (tot_s >= k) {
+                ltau = Ts;
+            }
+            mine = 0;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int j = lane + 64 * r;
+                mine += (j < cnt_w) && passes(bv[j], ltau, lstrict);
+            }
+            off = block_excl_scan(mine, n_s, S.wsum[1]);
+        }
         if (n_s > A.lcap) {
             // more ties at Ts than the list holds (fewer than k values lie above)
             lstrict = true;
@@ -1878,7 +1922,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
                 const int j = lane + 64 * r;
                 mine += (j < cnt_w) && passes(bv[j], ltau, true);
             }
-            off = block_excl_scan(mine, n_s, S.wsum[1]);
+            off = block_excl_scan(mine, n_s, S.wsum[0]);
         }
         // (fewer than k values lie above Ts or t*, and lcap > k; a list that
         // would still not fit is reported instead of written)
@@ -1951,18 +1995,18 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             return;
         }
         uint32_t kx = 0u, kn = 0xFFFFFFFFu;
-        for (int j = 0; j < nsl; ++j) {
-            const int o = offs[j];
-            const int n = ((j + 1 < nsl) ? offs[j + 1] : ntot) - o;
-            const size_t src = ((size_t)b * nsl + j) * A.lcap;
-            for (int i = tid; i < n; i += WG) {
-                const float v = dev_load(A.lst_val + src + i);
-                S.cval[o + i] = v;
-                S.cidx[o + i] = dev_load(A.lst_idx + src + i);
-                if (v == v) {
-                    kx = max(kx, fkey(v));
-                    kn = min(kn, fkey(v));
-                }
+        // every list at once (entry i of the concatenation -> its list j by
+        // the offsets), so that all loads are in flight together
+        for (int i = tid; i < ntot; i += WG) {
+            int j = 0;
+            while (j + 1 < nsl && offs[j + 1] <= i) ++j;
+            const size_t src = ((size_t)b * nsl + j) * A.lcap + (i - offs[j]);
+            const float v = dev_load(A.lst_val + src);
+            S.cval[i] = v;
+            S.cidx[i] = dev_load(A.lst_idx + src);
+            if (v == v) {
+                kx = max(kx, fkey(v));
+                kn = min(kn, fkey(v));
             }
         }
         kx = wave_max_u(kx);
