@@ -2668,13 +2668,16 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
     fetch_w(w1, rw, pw);
     if (++pw == npass) { pw = 0; ++rw; }                   // position of step 2
     int r = 0, p = 0;                                        // position of step s
-    for (int s = 0; s < nstep; ++s) {
+    // one step: compute on wc (step s), load step s+2 into wn; the three
+    // register sets rotate by unrolling, never by copies (a copy of a register
+    // still being loaded would wait for that load)
+    auto step = [&](int s, v4i (&wc)[4], v4i (&wn)[4]) {
         __syncthreads();  // step s's activations are in; the other buffer is free
         if (s + 1 < nstep) {
             stage_x(xr, (s + 1) & 1);
             if (s + 2 < nstep) fetch_x(xr, pw);
         }
-        fetch_w(w2, rw, pw);
+        fetch_w(wn, rw, pw);
         if (++pw == npass) { pw = 0; ++rw; }
         const int8_t *xb = xs[s & 1];
 #pragma unroll
@@ -2682,13 +2685,8 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const v4i a = *reinterpret_cast<const v4i *>(xb + ((mt * 4 + s4) * 64 + lane) * 16);
-                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, w0[s4], acc[mt], 0, 0, 0);
+                acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wc[s4], acc[mt], 0, 0, 0);
             }
-        }
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) {
-            w0[s4] = w1[s4];
-            w1[s4] = w2[s4];
         }
         if (++p == npass) {  // the tile's dot products are complete
             const int T = tlo + r * LMM_WAVES + wv;
@@ -2708,6 +2706,11 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
             p = 0;
             ++r;
         }
+    };
+    for (int s = 0; s < nstep; s += 3) {
+        step(s, w0, w2);
+        if (s + 1 < nstep) step(s + 1, w1, w0);
+        if (s + 2 < nstep) step(s + 2, w2, w1);
     }
 }
 
