@@ -821,6 +821,7 @@ __device__ __forceinline__ uint32_t block_kth_union(SM &S, int k, uint32_t kmin,
     }
     S.u.h.whist[0][threadIdx.x] = 0;
     S.u.h.whist[1][threadIdx.x] = 0;
+    S.u.h.whist[3][threadIdx.x] = 0;  // gather slots (see the final step)
     if (threadIdx.x == 0) S.gcount = 0;
     __syncthreads();
     const int L = __builtin_clz(kmin ^ kmax);
@@ -864,18 +865,14 @@ __device__ __forceinline__ uint32_t block_kth_union(SM &S, int k, uint32_t kmin,
             for (int r2 = 0; r2 < PK; ++r2)
                 if (key[r2] && (key[r2] & pmask) == prefix) gk[atomicAdd(&S.gcount, 1)] = key[r2];
             __syncthreads();
+            // slots past hb hold 0 (cleared at the start), below every
+            // live key: the loop covers only the gathered quads
             const uint32_t mine = (lane < hb) ? gk[lane] : 0u;
             int gt = 0, ge = 0;
-#pragma unroll
-            for (int q = 0; q < 16; ++q) {
+            for (int q = 0; q < ((hb + 3) >> 2); ++q) {
                 const uint4 v4 = reinterpret_cast<const uint4 *>(gk)[q];
-                const uint32_t vv[4] = {v4.x, v4.y, v4.z, v4.w};
-#pragma unroll
-                for (int c = 0; c < 4; ++c) {
-                    const bool in = 4 * q + c < hb;
-                    gt += (in && vv[c] > mine) ? 1 : 0;
-                    ge += (in && vv[c] >= mine) ? 1 : 0;
-                }
+                gt += (v4.x > mine) + (v4.y > mine) + (v4.z > mine) + (v4.w > mine);
+                ge += (v4.x >= mine) + (v4.y >= mine) + (v4.z >= mine) + (v4.w >= mine);
             }
             const unsigned long long fm = __ballot(lane < hb && gt < rem && rem <= ge);
             return (uint32_t)readlane_i((int)mine, fm ? (int)__builtin_ctzll(fm) : 0);
@@ -1271,24 +1268,28 @@ __device__ __forceinline__ Staged64 load_staged(const float *buf)
     return s;
 }
 
-// Sum of the 64 staged values in index order (entries past the set are +0.0).
-__device__ __forceinline__ float seq_total(const float *buf)
+// Sum of the staged values [0, n) in index order.  Entries from n to 63 are
+// +0.0, so the sum stops after the quad holding entry n - 1 (n is uniform).
+__device__ __forceinline__ float seq_total(const float *buf, int n)
 {
     const Staged64 s = load_staged(buf);
     float acc = 0.0f;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        acc = acc + s.q[i][0];
-        acc = acc + s.q[i][1];
-        acc = acc + s.q[i][2];
-        acc = acc + s.q[i][3];
+        if (4 * i < n) {
+            acc = acc + s.q[i][0];
+            acc = acc + s.q[i][1];
+            acc = acc + s.q[i][2];
+            acc = acc + s.q[i][3];
+        }
     }
     return acc;
 }
 
 // First index i < n whose inclusive sequential prefix reaches `target`
 // (prefix >= target); n if none.  The prefix never decreases (non-negative
-// terms), so the index is the number of prefixes that do not reach target.
+// terms), so the index is the number of prefixes that do not reach target,
+// clamped to n; prefixes past the quad holding entry n - 1 cannot change it.
 __device__ __forceinline__ int seq_first_reach(const float *buf, int n, float target)
 {
     const Staged64 s = load_staged(buf);
@@ -1296,10 +1297,12 @@ __device__ __forceinline__ int seq_first_reach(const float *buf, int n, float ta
     int below = 0;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
+        if (4 * i < n) {
 #pragma unroll
-        for (int c = 0; c < 4; ++c) {
-            acc = acc + s.q[i][c];
-            below += !(acc >= target) ? 1 : 0;  // a nan target is never reached
+            for (int c = 0; c < 4; ++c) {
+                acc = acc + s.q[i][c];
+                below += !(acc >= target) ? 1 : 0;  // a nan target is never reached
+            }
         }
     }
     return min(below, n);
@@ -1328,7 +1331,7 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
         e1 = valid ? glibc_expf((y - amax) / A.T, S.exptab) : 0.0f;
         buf[lane] = e1;
         wave_sync();
-        const float se = seq_total(buf);
+        const float se = seq_total(buf, nc);
         const float inv = 1.0f / (se + 1e-12f);
         const float p = valid ? e1 * inv : -1.0f;
         // rank in (probability desc, id asc) order: 64-bit keys, larger first
@@ -1337,8 +1340,7 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
         kb[lane] = key;  // 0 past the pool: below every valid key
         wave_sync();
         int rank = 0;
-#pragma unroll
-        for (int j = 0; j < 64; j += 2) {
+        for (int j = 0; j < nc; j += 2) {  // key 0 at nc (odd nc): below every valid key
             const ulonglong2 kk = reinterpret_cast<const ulonglong2 *>(kb)[j >> 1];
             rank += (kk.x > key) + (kk.y > key);
         }
@@ -1359,7 +1361,7 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
     const float e2 = !kept ? 0.0f : (top_p_on && mx == amax) ? e1 : glibc_expf((y - mx) / A.T, S.exptab);
     buf[lane] = e2;
     wave_sync();
-    const float sum = seq_total(buf);
+    const float sum = seq_total(buf, nc);
     RowResult res;
     res.n_kept = n_kept;
     res.sum = sum;
@@ -2107,8 +2109,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
                 if (lane >= nc) S.cidx[lane] = INT_MAX;
                 wave_sync();
                 int rank = 0;
-#pragma unroll
-                for (int q4 = 0; q4 < 16; ++q4) {
+                for (int q4 = 0; q4 < ((nc + 3) >> 2); ++q4) {
                     const int4 v = reinterpret_cast<const int4 *>(S.cidx)[q4];
                     rank += (v.x < myid) + (v.y < myid) + (v.z < myid) + (v.w < myid);
                 }
