@@ -524,23 +524,25 @@ struct RowCtx {
     bool has_bias, has_allow, use_hash;
 };
 
+// exact value of id e from its upper bound yhat, given its hash slot s (-1:
+// not in the hash, and the bound is exact)
+__device__ __forceinline__ float exact_at_slot(const RowCtx &R, int e, float yhat, int s)
+{
+    if (s < 0) return yhat;
+    const int info = R.hinfo[s];
+    // without a bias the upper bound is the raw logit (or -inf when the allow
+    // bit is clear, which the mask below keeps)
+    const float raw = R.has_bias ? R.row[e] : yhat;
+    float y = penalise(raw, info & HCOUNT_MASK, R.pen);
+    if (R.has_bias) y = y + R.bias[e];
+    if (R.has_allow && !allow_bit(R.abits, e)) y = -INFINITY;
+    if (info & HF_MASKPRE) y = -INFINITY;
+    return y;
+}
+
 __device__ __forceinline__ float exact_value(const RowCtx &R, int e, float yhat)
 {
-    if (R.use_hash) {
-        const int s = hash_find(R.hkey, e);
-        if (s >= 0) {
-            const int info = R.hinfo[s];
-            // without a bias the upper bound is the raw logit (or -inf when
-            // the allow bit is clear, which the mask below keeps)
-            const float raw = R.has_bias ? R.row[e] : yhat;
-            float y = penalise(raw, info & HCOUNT_MASK, R.pen);
-            if (R.has_bias) y = y + R.bias[e];
-            if (R.has_allow && !allow_bit(R.abits, e)) y = -INFINITY;
-            if (info & HF_MASKPRE) y = -INFINITY;
-            return y;
-        }
-    }
-    return yhat;
+    return exact_at_slot(R, e, yhat, R.use_hash ? hash_find(R.hkey, e) : -1);
 }
 
 // k-th largest of the 64 lane keys (1 <= k <= 64), bit by bit: the largest K
@@ -633,6 +635,47 @@ __device__ __forceinline__ void wave_refine(float *bv, int *bi, int cnt, const R
         const float y = exact_value(R, e, bv[j]);
         bv[j] = passes(y, tau, strict) ? y : NAN;
         bi[j] = e;
+    }
+    wave_sync();
+}
+
+// wave_refine for the end of the stream, when the stream's registers are
+// free (inside the stream loop the extra registers would spill).
+__device__ __forceinline__ void wave_refine_batched(float *bv, int *bi, int cnt, const RowCtx &R, float tau,
+                                                    bool strict)
+{
+    // eight entries per lane at a time: their buffer reads, then their first
+    // hash probes, are in flight together (linear probing rarely goes on)
+    constexpr int RB = 8;
+    const int lane = lane_id();
+    for (int j0 = 0; j0 < cnt; j0 += RB * 64) {
+        int id[RB], slot[RB], key[RB];
+        float yh[RB];
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            const int j = j0 + r * 64 + lane;
+            id[r] = (j < cnt) ? bi[j] : 0;
+            yh[r] = (j < cnt) ? bv[j] : NAN;
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            slot[r] = (int)hslot(id[r] & ~UNREFINED);
+            key[r] = (id[r] & UNREFINED) ? R.hkey[slot[r]] : -1;
+        }
+#pragma unroll
+        for (int r = 0; r < RB; ++r) {
+            if (!(id[r] & UNREFINED)) continue;
+            const int e = id[r] & ~UNREFINED;
+            int sl = slot[r], k = key[r];
+            for (int probe = 1; probe < HSLOTS && k != e && k != -1; ++probe) {
+                sl = (sl + 1) & (HSLOTS - 1);
+                k = R.hkey[sl];
+            }
+            const float y = exact_at_slot(R, e, yh[r], k == e ? sl : -1);
+            const int j = j0 + r * 64 + lane;
+            bv[j] = passes(y, tau, strict) ? y : NAN;
+            bi[j] = e;
+        }
     }
     wave_sync();
 }
@@ -1795,7 +1838,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
     // resolve the entries still holding upper bounds (below the estimate:
     // dropped, so the count below verifies it)
-    if (use_hash) wave_refine(bv, bi, st.cnt, R, tau_est, false);
+    if (use_hash) wave_refine_batched(bv, bi, st.cnt, R, tau_est, false);
     int alive = 0;
     uint32_t kx = 0u, kn = 0xFFFFFFFFu;  // range of the live keys
     for (int j = lane; j < st.cnt; j += 64) {
