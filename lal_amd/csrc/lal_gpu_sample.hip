@@ -2642,7 +2642,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_mfma_kernel(const int8
 // steps of w in flight across tile boundaries; the activations of a step are
 // staged in LDS one step ahead, their global loads issued before the w loads
 // of the same step (loads complete in issue order).  Batch rows 1..64.
-template <int MT>
+template <int MT, int PD>
 __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const int8_t *xq, const float *sx, int n,
                                                                         const int8_t *wpk, const float *sw, int V,
                                                                         float *logits, int ld, int b0, int nb)
@@ -2673,16 +2673,21 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
             xr[j] = v;
         }
     };
-    // staged in A-operand order: the 16 bytes lane l of wave-instruction
-    // (mt, s4) reads sit at ((mt*4 + s4)*64 + l)*16, so each read is one
-    // contiguous 1 KB (no bank conflicts)
+    // staged in A-operand order: the 16 bytes lane l = 16 g + r of
+    // wave-instruction (mt, s4) reads sit in that instruction's 1 KB block at
+    // slot 16 g + ((r + 4 g + s4) & 15).  The rotation keeps both sides free
+    // of bank conflicts: the 16 chunks of one activation row (4 g + s4 =
+    // 0..15) land in 16 different 16-byte bank groups, and the 16 lanes of a
+    // read pass read a permutation of one 256-byte line.
     auto stage_x = [&](const v4i (&xr)[XPT], int buf) {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
             const int c = tid + j * 64 * LMM_WAVES;
             if (c < XCH) {
                 const int row = c / (LMM_KC / 16), c16 = c % (LMM_KC / 16);
-                const int dst = (((row >> 4) * 4 + (c16 >> 2)) * 64 + (c16 & 3) * 16 + (row & 15)) * 16;
+                const int gg = c16 & 3, s4 = c16 >> 2;
+                const int slot = gg * 16 + (((row & 15) + 4 * gg + s4) & 15);
+                const int dst = (((row >> 4) * 4 + s4) * 64 + slot) * 16;
                 *reinterpret_cast<v4i *>(&xs[buf][dst]) = xr[j];
             }
         }
@@ -2702,33 +2707,43 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
     v4i acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
-    v4i w0[4], w1[4], w2[4];
+    v4i w0[4], w1[4], w2[4], w3[4];
     v4i xr[XPT];
     fetch_x(xr, 0);
     stage_x(xr, 0);
     fetch_x(xr, 1 % npass);  // activations of step 1, ahead of every w load
-    fetch_w(w0, 0, 0);
-    int rw = (npass > 1) ? 0 : 1, pw = (npass > 1) ? 1 : 0;  // position of step 1
+    // w of the first PD steps; (rw, pw) then holds the position of step PD
+    int rw = 0, pw = 0;
+    auto advance = [&]() {
+        if (++pw == npass) { pw = 0; ++rw; }
+    };
+    fetch_w(w0, rw, pw);
+    advance();
     fetch_w(w1, rw, pw);
-    if (++pw == npass) { pw = 0; ++rw; }                   // position of step 2
+    advance();
+    if (PD == 3) {
+        fetch_w(w2, rw, pw);
+        advance();
+    }
     int r = 0, p = 0;                                        // position of step s
-    // one step: compute on wc (step s), load step s+2 into wn; the three
+    // one step: compute on wc (step s), load step s+PD into wn; the PD + 1
     // register sets rotate by unrolling, never by copies (a copy of a register
     // still being loaded would wait for that load)
     auto step = [&](int s, v4i (&wc)[4], v4i (&wn)[4]) {
         __syncthreads();  // step s's activations are in; the other buffer is free
         if (s + 1 < nstep) {
             stage_x(xr, (s + 1) & 1);
-            if (s + 2 < nstep) fetch_x(xr, pw);
+            if (s + 2 < nstep) fetch_x(xr, (s + 2) % npass);  // activations of step s+2
         }
         fetch_w(wn, rw, pw);
-        if (++pw == npass) { pw = 0; ++rw; }
+        advance();
         const int8_t *xb = xs[s & 1];
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
+            const int slot = g * 16 + ((r16 + 4 * g + s4) & 15);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
-                const v4i a = *reinterpret_cast<const v4i *>(xb + ((mt * 4 + s4) * 64 + lane) * 16);
+                const v4i a = *reinterpret_cast<const v4i *>(xb + ((mt * 4 + s4) * 64 + slot) * 16);
                 acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wc[s4], acc[mt], 0, 0, 0);
             }
         }
@@ -2751,10 +2766,19 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
             ++r;
         }
     };
-    for (int s = 0; s < nstep; s += 3) {
-        step(s, w0, w2);
-        if (s + 1 < nstep) step(s + 1, w1, w0);
-        if (s + 2 < nstep) step(s + 2, w2, w1);
+    if (PD == 2) {
+        for (int s = 0; s < nstep; s += 3) {
+            step(s, w0, w2);
+            if (s + 1 < nstep) step(s + 1, w1, w0);
+            if (s + 2 < nstep) step(s + 2, w2, w1);
+        }
+    } else {
+        for (int s = 0; s < nstep; s += 4) {
+            step(s, w0, w3);
+            if (s + 1 < nstep) step(s + 1, w1, w0);
+            if (s + 2 < nstep) step(s + 2, w2, w1);
+            if (s + 3 < nstep) step(s + 3, w3, w2);
+        }
     }
 }
 
@@ -3661,12 +3685,21 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
         if (const char *env = getenv("LAL_GPU_LMH_WG")) per_cu = std::max(1, atoi(env));
         const unsigned nwg = (unsigned)std::max(1, std::min(per_cu * ctx->ncu, (ntile + LMM_WAVES - 1) / LMM_WAVES));
         const dim3 g2(nwg), blk(64 * LMM_WAVES);
-        switch (mt) {
-        case 1: hipLaunchKernelGGL(lm_head_packed_kernel<1>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb); break;
-        case 2: hipLaunchKernelGGL(lm_head_packed_kernel<2>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb); break;
-        case 3: hipLaunchKernelGGL(lm_head_packed_kernel<3>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb); break;
-        default: hipLaunchKernelGGL(lm_head_packed_kernel<4>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb); break;
+        int pd = (mt <= 2) ? 2 : 3;  // W steps in flight per wave
+        if (const char *env = getenv("LAL_GPU_LMH_PD")) pd = (atoi(env) == 3) ? 3 : 2;
+#define LAL_LMH(M, D) \
+    hipLaunchKernelGGL((lm_head_packed_kernel<M, D>), g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb)
+        switch (mt * 4 + pd) {
+        case 6: LAL_LMH(1, 2); break;
+        case 7: LAL_LMH(1, 3); break;
+        case 10: LAL_LMH(2, 2); break;
+        case 11: LAL_LMH(2, 3); break;
+        case 14: LAL_LMH(3, 2); break;
+        case 15: LAL_LMH(3, 3); break;
+        case 18: LAL_LMH(4, 2); break;
+        default: LAL_LMH(4, 3); break;
         }
+#undef LAL_LMH
         LAL_HIP(hipGetLastError());
     }
     return LAL_GPU_OK;
