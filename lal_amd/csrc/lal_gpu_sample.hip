@@ -2675,10 +2675,11 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
     };
     // staged in A-operand order: the 16 bytes lane l = 16 g + r of
     // wave-instruction (mt, s4) reads sit in that instruction's 1 KB block at
-    // slot 16 g + ((r + 4 g + s4) & 15).  The rotation keeps both sides free
-    // of bank conflicts: the 16 chunks of one activation row (4 g + s4 =
-    // 0..15) land in 16 different 16-byte bank groups, and the 16 lanes of a
-    // read pass read a permutation of one 256-byte line.
+    // slot 16 g + ((r + g + 4 s4) & 15).  The rotation keeps both sides free
+    // of bank conflicts: any 8 consecutive chunks of one activation row
+    // (g + 4 s4 = 0..7 or 8..15) land in 8 different 16-byte groups of a
+    // 128-byte bank line, and the lanes of a read pass read consecutive
+    // slots.
     auto stage_x = [&](const v4i (&xr)[XPT], int buf) {
 #pragma unroll
         for (int j = 0; j < XPT; ++j) {
@@ -2686,7 +2687,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
             if (c < XCH) {
                 const int row = c / (LMM_KC / 16), c16 = c % (LMM_KC / 16);
                 const int gg = c16 & 3, s4 = c16 >> 2;
-                const int slot = gg * 16 + (((row & 15) + 4 * gg + s4) & 15);
+                const int slot = gg * 16 + (((row & 15) + gg + 4 * s4) & 15);
                 const int dst = (((row >> 4) * 4 + s4) * 64 + slot) * 16;
                 *reinterpret_cast<v4i *>(&xs[buf][dst]) = xr[j];
             }
@@ -2740,7 +2741,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
         const int8_t *xb = xs[s & 1];
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
-            const int slot = g * 16 + ((r16 + 4 * g + s4) & 15);
+            const int slot = g * 16 + ((r16 + g + 4 * s4) & 15);
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) {
                 const v4i a = *reinterpret_cast<const v4i *>(xb + ((mt * 4 + s4) * 64 + slot) * 16);
