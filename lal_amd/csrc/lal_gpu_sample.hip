@@ -1631,6 +1631,19 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     const int vlen = 4 * (se - sb) + (has_extras ? g.head + g.ntail : 0);
     const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
 
+    f32x4 cur[U4], nx1[U4];
+    // few workgroups (a small batch): the first two stream iterations go out
+    // with the sample, nothing queues behind them
+    const bool early = A.batch <= 16;
+    if (early) {
+#pragma unroll
+        for (int u = 0; u < U4; ++u) {
+            const int q = qb + u * 64 + lane;
+            cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+            const int q1 = qb + WITER + u * 64 + lane;
+            nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
+        }
+    }
     // the slice sample goes out first, alone: every workgroup waits for its
     // sample, and stream loads queued with it would only delay it
     f32x4 smp[SR];
@@ -1640,7 +1653,6 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const int q = sb + (sidx >> 6) * SBLK + (sidx & 63);
         smp[r] = (q < se) ? row4[q] : f32x4{NAN, NAN, NAN, NAN};
     }
-    f32x4 cur[U4], nx1[U4];
 
     // ---- setup: hash of history / ban ids, and the threshold estimate ----
     // tau_est = the ks-th largest of the per-thread maxima of the sampled
@@ -1674,12 +1686,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         skeys[tid] = (lm == lm && lm > -INFINITY) ? fkey(lm) : 0u;
     }
     // the first two iterations' loads fly during the hash setup and estimate
+    if (!early) {
 #pragma unroll
-    for (int u = 0; u < U4; ++u) {
-        const int q = qb + u * 64 + lane;
-        cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
-        const int q1 = qb + WITER + u * 64 + lane;
-        nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
+        for (int u = 0; u < U4; ++u) {
+            const int q = qb + u * 64 + lane;
+            cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
+            const int q1 = qb + WITER + u * 64 + lane;
+            nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
+        }
     }
     for (int s = tid; s < HSLOTS; s += WG) {
         S.hkey[s] = -1;
