@@ -2824,6 +2824,112 @@ __global__ __launch_bounds__(256) void quantize_w_kernel(const float *w, int n, 
     if (threadIdx.x == 0) scale[j] = s;
 }
 
+// Up to 16 batch rows with n <= LMX_MAXN: the activations of every pass stay
+// in LDS for the whole launch (staged once, in A-operand order with the slot
+// rotation of lm_head_packed_kernel, block kb per 64 k-bytes), so each wave
+// streams its tiles' W with three steps in flight and no barrier per step.
+// Same arithmetic as lm_head_packed_kernel<1, PD>.
+constexpr int LMX_MAXN = 4096;
+__global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(const int8_t *xq, const float *sx, int n,
+                                                                             const int8_t *wpk, const float *sw,
+                                                                             int V, float *logits, int ld, int b0,
+                                                                             int nb)
+{
+    __shared__ __align__(16) int8_t xs[16 * LMX_MAXN];
+    const int wv = wave_id(), lane = lane_id(), tid = threadIdx.x;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int npass = (n + LMM_KC - 1) / LMM_KC;
+    const int nc64 = (n + 63) / 64;  // 1 KB blocks per 16-row tile
+    const int ntile = (V + 15) / 16;
+    const int tlo = (int)(((long long)ntile * blockIdx.x) / gridDim.x);
+    const int thi = (int)(((long long)ntile * (blockIdx.x + 1)) / gridDim.x);
+    const int nround = (thi - tlo + LMM_WAVES - 1) / LMM_WAVES;
+    const int nstep = nround * npass;
+
+    // w of (round r, pass p): this wave's tile, blocks 4p .. 4p+3
+    auto fetch_w = [&](v4i (&f)[4], int r, int p) {
+        const int T = tlo + r * LMM_WAVES + wv;
+        const bool ok = r < nround && T < thi;
+        const v4i *base = reinterpret_cast<const v4i *>(wpk + ((size_t)(ok ? T : 0) * nc64) * 1024) + lane;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const int c = 4 * p + s4;
+            f[s4] = (ok && c < nc64) ? __builtin_nontemporal_load(base + (size_t)c * 64) : v4i{0, 0, 0, 0};
+        }
+    };
+    // the activations (chunk c = (row, c16), 16 bytes at k = 16 c16 of row
+    // c / (4 nc64)) are loaded first, then the first three steps' W, then the
+    // activations are stored to LDS (loads complete in issue order)
+    constexpr int XR = 16 * (LMX_MAXN / 16) / (64 * LMM_WAVES);
+    const int cpr = 4 * nc64;
+    v4i xr[XR];
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c = tid + j * 64 * LMM_WAVES;
+        const int row = c / cpr, k = 16 * (c - row * cpr);
+        v4i v = {0, 0, 0, 0};
+        if (c < 16 * cpr && row < nb && k < n) v = *reinterpret_cast<const v4i *>(xq + (size_t)(b0 + row) * n + k);
+        xr[j] = v;
+    }
+    v4i w0[4], w1[4], w2[4], w3[4];
+    int rw = 0, pw = 0;
+    auto advance = [&]() {
+        if (++pw == npass) { pw = 0; ++rw; }
+    };
+    fetch_w(w0, rw, pw);
+    advance();
+    fetch_w(w1, rw, pw);
+    advance();
+    fetch_w(w2, rw, pw);
+    advance();
+#pragma unroll
+    for (int j = 0; j < XR; ++j) {
+        const int c = tid + j * 64 * LMM_WAVES;
+        if (c < 16 * cpr) {
+            const int row = c / cpr, c16 = c - row * cpr;
+            const int gg = c16 & 3, kb = c16 >> 2;
+            const int slot = gg * 16 + ((row + gg + 4 * (kb & 3)) & 15);
+            *reinterpret_cast<v4i *>(&xs[(kb * 64 + slot) * 16]) = xr[j];
+        }
+    }
+    __syncthreads();
+    if (nstep == 0) return;
+
+    v4i acc = {0, 0, 0, 0};
+    int r = 0, p = 0;  // position of step s
+    auto step = [&](v4i (&wc)[4], v4i (&wn)[4]) {
+        fetch_w(wn, rw, pw);  // step s + 3
+        advance();
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const int slot = g * 16 + ((r16 + g + 4 * s4) & 15);
+            const v4i a = *reinterpret_cast<const v4i *>(xs + ((4 * p + s4) * 64 + slot) * 16);
+            acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wc[s4], acc, 0, 0, 0);
+        }
+        if (++p == npass) {  // the tile's dot products are complete
+            const int T = tlo + r * LMM_WAVES + wv;
+            const int v = 16 * T + r16;
+            if (T < thi && v < V) {
+                const float swv = sw[v];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int bb = 4 * g + i;
+                    if (bb < nb) logits[(size_t)(b0 + bb) * ld + v] = (sx[b0 + bb] * swv) * (float)acc[i];
+                }
+            }
+            acc = v4i{0, 0, 0, 0};
+            p = 0;
+            ++r;
+        }
+    };
+    for (int s = 0; s < nstep; s += 4) {
+        step(w0, w3);
+        if (s + 1 < nstep) step(w1, w0);
+        if (s + 2 < nstep) step(w2, w1);
+        if (s + 3 < nstep) step(w3, w2);
+    }
+}
+
 // Row-major int8 [V][n] -> packed layout (one thread per 16 bytes).
 __global__ __launch_bounds__(256) void pack_q8_kernel(const int8_t *w, int V, int n, int8_t *wpk)
 {
@@ -3696,10 +3802,19 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
     for (int b0 = 0; b0 < batch; b0 += LMM_MAXB) {
         const int nb = std::min(LMM_MAXB, batch - b0);
         const int mt = (nb + 15) / 16;
-        int per_cu = (mt <= 2) ? 4 : 2;  // workgroups per CU (measured best at each tile height)
+        // up to 16 rows: the activations resident in LDS (64 KB: 2 workgroups per CU)
+        bool xres = mt == 1 && n <= LMX_MAXN;
+        if (const char *env = getenv("LAL_GPU_LMH_XRES")) xres = xres && atoi(env) != 0;
+        int per_cu = xres ? 2 : (mt <= 2) ? 4 : 2;  // workgroups per CU (measured best at each shape)
         if (const char *env = getenv("LAL_GPU_LMH_WG")) per_cu = std::max(1, atoi(env));
         const unsigned nwg = (unsigned)std::max(1, std::min(per_cu * ctx->ncu, (ntile + LMM_WAVES - 1) / LMM_WAVES));
         const dim3 g2(nwg), blk(64 * LMM_WAVES);
+        if (xres) {
+            hipLaunchKernelGGL(lm_head_packed_xres_kernel, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits,
+                               ld, b0, nb);
+            LAL_HIP(hipGetLastError());
+            continue;
+        }
         int pd = (mt <= 2) ? 2 : 3;  // W steps in flight per wave
         if (const char *env = getenv("LAL_GPU_LMH_PD")) pd = (atoi(env) == 3) ? 3 : 2;
 #define LAL_LMH(M, D) \

@@ -191,6 +191,24 @@ def test_lm_head_packed(dev, orc, B):
     log(f"packed lm_head B={B}: {B} x {V} bit-exact")
 
 
+@pytest.mark.parametrize("B,n", [(1, 3408), (16, 3408), (5, 4096), (7, 4160)])
+def test_lm_head_packed_activation_widths(dev, orc, B, n):
+    """Up to 16 rows the activations stay in LDS for the whole launch when
+    n <= 4096: n = 3408 leaves a partial 64-byte k-group (zero-staged), n =
+    4096 fills the buffer, n = 4160 takes the per-step staging instead."""
+    V = 4099
+    rng = np.random.default_rng(2000 + B + n)
+    W = rng.integers(-127, 128, (V, n)).astype(np.int8)
+    sw = (rng.random(V) * 0.019 + 0.001).astype(np.float32)
+    x = synth.normal(270 + B, 0, B * n).reshape(B, n).astype(np.float32)
+    s, q = quantize(dev, x, 0)
+    out, _ = lm_head_packed(dev, q, s, W, sw)
+    for b in range(B):
+        want = orc.lm_head(q[b].copy(), s[b], W, sw)
+        assert np.array_equal(out[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
+    log(f"packed lm_head B={B} n={n}: bit-exact")
+
+
 def test_pack_layout_ragged(dev):
     """Shapes that are not multiples of 16 rows or 64 bytes pack with zeros."""
     for V, n in ((1, 16), (17, 80), (37, 200), (5, 1000)):
