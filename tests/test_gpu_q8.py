@@ -172,11 +172,12 @@ def test_lm_head_matrix_core_path(dev, orc, B):
     log(f"matrix-core lm_head B={B}: {B} x {V} bit-exact")
 
 
-@pytest.mark.parametrize("B", [1, 3, 9, 16, 33, 64, 100])
+@pytest.mark.parametrize("B", [1, 3, 9, 16, 33, 64, 70, 100])
 def test_lm_head_packed(dev, orc, B):
     """The packed weight layout (lal_gpu_pack_q8) against its definition, and
     lal_gpu_lm_head_q8_packed bit-exact against the oracle on every logit
-    (V = 5003 leaves a partial 16-row tile, n = 3392 a partial 256-byte pass)."""
+    (V = 5003 leaves a partial 16-row tile, n = 3392 a partial 256-byte pass;
+    B = 70 and 100 run a second launch from row 64)."""
     V, n = 5003, 3392
     rng = np.random.default_rng(1000 + B)
     W = rng.integers(-127, 128, (V, n)).astype(np.int8)
