@@ -2836,6 +2836,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
                                                                              int nb)
 {
     __shared__ __align__(16) int8_t xs[16 * LMX_MAXN];
+    __shared__ __align__(16) float ot[LMM_WAVES][16 * 16];  // a finished tile, row-major
     const int wv = wave_id(), lane = lane_id(), tid = threadIdx.x;
     const int g = lane >> 4, r16 = lane & 15;
     const int npass = (n + LMM_KC - 1) / LMM_KC;
@@ -2895,6 +2896,11 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     __syncthreads();
     if (nstep == 0) return;
 
+    // the scales of this lane's 4 batch rows, loaded once
+    float sxr[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sxr[i] = (4 * g + i < nb) ? sx[b0 + 4 * g + i] : 0.0f;
+    const bool vec_out = ((ld & 3) == 0) && ((((uintptr_t)logits) & 15) == 0);
     v4i acc = {0, 0, 0, 0};
     int r = 0, p = 0;  // position of step s
     auto step = [&](v4i (&wc)[4], v4i (&wn)[4]) {
@@ -2908,14 +2914,41 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
         }
         if (++p == npass) {  // the tile's dot products are complete
             const int T = tlo + r * LMM_WAVES + wv;
-            const int v = 16 * T + r16;
-            if (T < thi && v < V) {
-                const float swv = sw[v];
+            if (T < thi && nb <= 4) {
+                const int v = 16 * T + r16;
+                if (v < V) {
+                    const float swv = sw[v];
 #pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int bb = 4 * g + i;
-                    if (bb < nb) logits[(size_t)(b0 + bb) * ld + v] = (sx[b0 + bb] * swv) * (float)acc[i];
+                    for (int i = 0; i < 4; ++i) {
+                        const int bb = 4 * g + i;
+                        if (bb < nb) logits[(size_t)(b0 + bb) * ld + v] = (sxr[i] * swv) * (float)acc[i];
+                    }
                 }
+            } else if (T < thi) {
+                // lane (g, r16) holds rows 4g..4g+3 of vocab row 16T + r16; a
+                // pass through LDS gives lane l row l/4, vocab 16T + 4(l%4) ..
+                // +3, so that the tile leaves in one 16-byte store per lane
+                // instead of four scattered ones (the store count, not the
+                // bytes, costs at 5-16 rows)
+                const int v = 16 * T + r16;
+                const float swv = (v < V) ? sw[v] : 0.0f;
+                float *o = ot[wv];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[(4 * g + i) * 16 + r16] = (sxr[i] * swv) * (float)acc[i];
+                wave_sync();
+                const int R = lane >> 2, v0 = 16 * T + 4 * (lane & 3);
+                const f32x4 val = *reinterpret_cast<const f32x4 *>(o + R * 16 + 4 * (lane & 3));
+                if (R < nb) {
+                    float *dst = logits + (size_t)(b0 + R) * ld + v0;
+                    if (vec_out && v0 + 3 < V) {
+                        *reinterpret_cast<f32x4 *>(dst) = val;
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            if (v0 + c < V) dst[c] = val[c];
+                    }
+                }
+                wave_sync();  // the tile buffer is read before the next tile writes it
             }
             acc = v4i{0, 0, 0, 0};
             p = 0;
