@@ -2662,6 +2662,8 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
                                                                         float *logits, int ld, int b0, int nb)
 {
     __shared__ __align__(16) int8_t xs[2][MT * 16 * LMM_KC];
+    // a finished tile (MT*16 rows x 16 vocab, row-major) on its way out
+    __shared__ __align__(16) float ot[MT > 1 ? LMM_WAVES : 1][MT > 1 ? MT * 256 : 4];
     constexpr int XCH = MT * 16 * (LMM_KC / 16);
     constexpr int XPT = (XCH + 64 * LMM_WAVES - 1) / (64 * LMM_WAVES);
     const int wv = wave_id(), lane = lane_id(), tid = threadIdx.x;
@@ -2722,6 +2724,16 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
     v4i acc[MT];
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+    // the scales of this lane's batch rows (MT > 1), loaded once
+    float sxr[MT][4];
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const int bb = mt * 16 + 4 * g + i;
+            sxr[mt][i] = (MT > 1 && bb < nb) ? sx[b0 + bb] : 0.0f;
+        }
+    const bool vec_out = ((ld & 3) == 0) && ((((uintptr_t)logits) & 15) == 0);
     v4i w0[4], w1[4], w2[4], w3[4];
     v4i xr[XPT];
     fetch_x(xr, 0);
@@ -2765,15 +2777,41 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
         if (++p == npass) {  // the tile's dot products are complete
             const int T = tlo + r * LMM_WAVES + wv;
             const int v = 16 * T + r16;
-            if (T < thi && v < V) {
+            if (MT == 1 && T < thi && v < V) {
                 const float swv = sw[v];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int bb = 4 * g + i;
+                    if (bb < nb) logits[(size_t)(b0 + bb) * ld + v] = (sx[b0 + bb] * swv) * (float)acc[0][i];
+                }
+            } else if (MT > 1 && T < thi) {
+                // through LDS, so that lane l stores float4 f = 64 q + l of the
+                // tile (row f/4, vocab 16T + 4(f%4) ..), MT 16-byte stores per
+                // lane instead of 4 MT scattered ones
+                const float swv = (v < V) ? sw[v] : 0.0f;
+                float *o = ot[MT > 1 ? wv : 0];
 #pragma unroll
                 for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-                    for (int i = 0; i < 4; ++i) {
-                        const int bb = mt * 16 + 4 * g + i;
-                        if (bb < nb) logits[(size_t)(b0 + bb) * ld + v] = (sx[b0 + bb] * swv) * (float)acc[mt][i];
+                    for (int i = 0; i < 4; ++i)
+                        o[(mt * 16 + 4 * g + i) * 16 + r16] = (sxr[mt][i] * swv) * (float)acc[mt][i];
+                wave_sync();
+#pragma unroll
+                for (int q = 0; q < MT; ++q) {
+                    const int f = q * 64 + lane, row = f >> 2, v0 = 16 * T + 4 * (f & 3);
+                    const f32x4 val = *reinterpret_cast<const f32x4 *>(o + row * 16 + 4 * (f & 3));
+                    if (row < nb) {
+                        float *dst = logits + (size_t)(b0 + row) * ld + v0;
+                        if (vec_out && v0 + 3 < V) {
+                            *reinterpret_cast<f32x4 *>(dst) = val;
+                        } else {
+#pragma unroll
+                            for (int c = 0; c < 4; ++c)
+                                if (v0 + c < V) dst[c] = val[c];
+                        }
                     }
+                }
+                wave_sync();  // the tile buffer is read before the next tile writes it
             }
 #pragma unroll
             for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
