@@ -179,6 +179,23 @@ def test_top_p(run, orc, top_p, kind):
         assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=512)
 
 
+@pytest.mark.parametrize("k", [1, 2, 3, 5, 62, 63, 64, 65])
+def test_pool_sizes_at_the_wave_edge(run, orc, k):
+    """Pools of 1-5 and 62-65 entries: the one-wave epilogue's loops run over
+    the pool's quads only (sums, first-reach, id and probability ranks), and 65
+    entries take the block epilogue; draws at both ends of [0, 1]."""
+    B, V = 8, 24001
+    x = np.stack([synth.make_row("gauss" if b % 2 else "zipf", 41 * b + k, V) for b in range(B)])
+    hist = synth.history(16, B, 24, V)
+    u = np.array([0.0, 1.0, 0.5, 1e-7, 0.999999, 0.25, 0.75, 0.33], np.float32)
+    for top_p in (0.0, 0.5, 0.95):
+        for variant in (0, 1):
+            kw = dict(T=0.85, k=k, top_p=top_p, pen=1.1, variant=variant, hist=hist, u=u,
+                      cand_ld=128)
+            log(f"pool edge k {k} top_p {top_p} variant {variant}")
+            assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=128)
+
+
 def test_bans_and_gpt2_draw(run, orc):
     from lal_amd import abi
     B, V = 16, 4099
