@@ -42,7 +42,7 @@
 extern "C" {
 #endif
 
-#define LAL_GPU_ABI_VERSION 2
+#define LAL_GPU_ABI_VERSION 3
 
 /* Limits.  top_k is capped at 512, the largest heap the reference samplers
  * hold (tools/server/qwen7b_server.c:239); beyond it the reference is
@@ -70,14 +70,35 @@ extern "C" {
 #define LAL_GPU_F_WRITEBACK  0x1u /* write the penalised value back into
                                      logits[row][t] for every history id t, the
                                      reference's in-place side effect */
-#define LAL_GPU_F_DRAW_GPT2  0x2u /* gpt2_server.c:2997-3002 draw: r == 0
-                                     returns token 0 */
+#define LAL_GPU_F_DRAW_GPT2  0x2u /* the draw scans every id with cum += e_v
+                                     (0 for ids not kept), so r == 0 returns
+                                     token 0: gpt2_server.c:2997-3002 and
+                                     qwen_server.c:518-524 */
+#define LAL_GPU_F_DRAW_ALL_IDS LAL_GPU_F_DRAW_GPT2
+#define LAL_GPU_F_FALLBACK_ZERO 0x4u /* when no running sum reaches r (a nan
+                                     sum), return 0 instead of vocab-1
+                                     (tools/mini_server.c:339-347) */
+#define LAL_GPU_F_GREEDY_FILTER 0x8u /* greedy rows go through the lal_filter_topk
+                                     bans too, as mini_server.c:284-288 passes
+                                     the argmax as a one-element keep mask
+                                     (&km): a ban of id 0 makes the token 0
+                                     (bans of other ids fall outside that
+                                     one-element array and do nothing) */
+
+/* The other reference samplers as parameter sets:
+ *   tools/server/qwen_server.c:418-527 sample_next_token
+ *       VARIANT_BASIC | F_DRAW_ALL_IDS (no sum <= 0 branch; r == 0 -> id 0)
+ *   tools/mini_server.c:267-363 sample_next_token
+ *       VARIANT_FILTERED | F_FALLBACK_ZERO | F_GREEDY_FILTER, without
+ *       F_WRITEBACK (it penalises a copy of the row), io.last_tokens = the
+ *       caller's last token (it is not recent[n-1] once its 256-entry recent
+ *       array is full) */
 
 typedef struct lal_gpu_ctx lal_gpu_ctx;
 
 typedef struct lal_gpu_sample_params {
     float temperature;  /* <= 0: greedy (first index of the maximum) */
-    int   top_k;        /* <= 0: greedy; clamped to vocab; <= LAL_GPU_MAX_K */
+    int   top_k;        /* <= 0: greedy; clamped to vocab, then <= LAL_GPU_MAX_K */
     float top_p;        /* nucleus over the top-k pool when 0 < top_p < 1 */
     float rep_penalty;  /* applied when > 1: x>0 ? x/p : x*p per occurrence */
     int   variant;      /* LAL_GPU_VARIANT_* */
@@ -118,6 +139,10 @@ typedef struct lal_gpu_sample_io {
     float          *out_history_vals; /* [batch][history_ld] logits[t] after the
                                          penalty for each history position */
     float          *cand_vals;     /* [batch][cand_ld] processed logit of each pool id */
+    /* optional input (device): [batch] the token ban_last drops, in place of
+     * history[len-1] (mini_server.c passes its last token separately); NULL:
+     * history[len-1] */
+    const int      *last_tokens;
 } lal_gpu_sample_io;
 
 /* Finish over a pool filtered on the host: the keep-mask half of
@@ -150,12 +175,17 @@ typedef struct lal_gpu_finish_io {
  * per row).  One context per host thread / stream: calls that overlap on one
  * context race.  Rows may be split into slices, one workgroup each, when the
  * batch is too small to fill the GPU; the environment variable
- * LAL_GPU_SLICES (1..64) overrides that choice (tuning only; results do not
- * depend on it). */
+ * LAL_GPU_SLICES (1..64), read when the context is created, overrides that
+ * choice (tuning only; results do not depend on it). */
 int  lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab);
 void lal_gpu_destroy(lal_gpu_ctx *ctx);
 
-/* Batched sampler: one token per row. */
+/* Batched sampler: one token per row.  Rows may hold any float values:
+ * -inf, +inf and nan are handled as the reference's comparisons treat them
+ * (a nan never enters the pool; a row with nans takes an exact, slower path
+ * that replays the reference's heap).  out_token[b] = -1 would report an
+ * internal capacity error; the library's bounds exclude it (a returned
+ * LAL_GPU_OK never comes with -1), and callers may treat -1 as fatal. */
 int  lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab,
                     const lal_gpu_sample_params *params,
                     const lal_gpu_sample_io *io, void *stream);

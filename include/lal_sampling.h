@@ -85,6 +85,8 @@ typedef struct {
     int *d_hist, *d_tok, *d_ban;
     float *d_u, *d_sum, *d_hvals;
     int ban_last, ban_repeat, n_ban;
+    int h_ban[LAL_GPU_MAX_BAN_IDS];  /* host copy, uploaded again when the
+                                        device buffers are re-created */
     /* keep-mask adapter for a loaded lal_filter_topk plugin */
     lal_filter_topk_fn plugin;
     lal_token_decode_fn decode;
@@ -166,6 +168,11 @@ static void lal__ensure(int vocab)
     LAL__CHECK(lal_gpu_malloc((void **)&g->d_ncand, sizeof(int)), "lal_gpu_malloc");
     LAL__CHECK(lal_gpu_malloc((void **)&g->d_cvals, (size_t)vocab * sizeof(float)), "lal_gpu_malloc");
     LAL__CHECK(lal_gpu_malloc((void **)&g->d_keep, (size_t)vocab), "lal_gpu_malloc");
+    if (g->n_ban > 0) {
+        LAL__CHECK(lal_gpu_memcpy_h2d(g->d_ban, g->h_ban, (size_t)g->n_ban * sizeof(int), g->stream),
+                   "upload ban ids");
+        LAL__CHECK(lal_gpu_stream_sync(g->stream), "stream sync");
+    }
     g->h_mask = (int *)malloc((size_t)vocab * sizeof(int));
     g->h_cids = (int *)malloc((size_t)vocab * sizeof(int));
     g->h_keep = (unsigned char *)malloc((size_t)vocab);
@@ -177,12 +184,22 @@ static void lal__ensure(int vocab)
 /* One row through lal_gpu_sample.  Uploads the row and history, runs the
  * kernel with uniform u, and returns the token and softmax sum; the
  * penalised history values land in hvals[0..n_hist). */
-static int lal__run(const float *logits, int vocab, const lal_gpu_sample_params *p,
-                    const int *recent, int n_recent, float u, float *sum, float *hvals)
+static int lal__run_io(const float *logits, int vocab, const lal_gpu_sample_params *p,
+                       const int *recent, int n_recent, float u, float *sum, float *hvals,
+                       int with_pool)
 {
     lal_sampling_gpu_state *g = &lal__gs;
     lal_gpu_sample_io io;
     memset(&io, 0, sizeof io);
+    if (with_pool) {
+        /* the pool (ids ascending, processed logits, final kept flags) for a
+         * later lal_gpu_sample_finish; it can hold the whole row (ties) */
+        io.out_n_cand = g->d_ncand;
+        io.cand_ld = vocab;
+        io.cand_ids = g->d_cids;
+        io.cand_vals = g->d_cvals;
+        io.cand_kept = g->d_keep;
+    }
     LAL__CHECK(lal_gpu_memcpy_h2d(g->d_row, logits, (size_t)vocab * sizeof(float), g->stream),
                "upload logits");
     if (n_recent > 0) {
@@ -206,6 +223,37 @@ static int lal__run(const float *logits, int vocab, const lal_gpu_sample_params 
         LAL__CHECK(lal_gpu_memcpy_d2h(hvals, g->d_hvals, (size_t)n_recent * sizeof(float), g->stream),
                    "download history values");
     LAL__CHECK(lal_gpu_stream_sync(g->stream), "stream sync");
+    if (tok < 0) lal__die("lal_gpu_sample (internal capacity error, token -1)", LAL_GPU_E_RANGE);
+    return tok;
+}
+
+static int lal__run(const float *logits, int vocab, const lal_gpu_sample_params *p,
+                    const int *recent, int n_recent, float u, float *sum, float *hvals)
+{
+    return lal__run_io(logits, vocab, p, recent, n_recent, u, sum, hvals, 0);
+}
+
+/* The draw over the pool the last lal__run_io(with_pool) left on the device,
+ * with uniform u (the softmax and draw of qwen7b_server.c:275-294 over the
+ * kept flags the sampler computed): a pool-sized launch instead of a second
+ * upload and pass over the row. */
+static int lal__draw_pool(int vocab, const lal_gpu_sample_params *p, float u)
+{
+    lal_sampling_gpu_state *g = &lal__gs;
+    lal_gpu_finish_io fio;
+    memset(&fio, 0, sizeof fio);
+    LAL__CHECK(lal_gpu_memcpy_h2d(g->d_u, &u, sizeof u, g->stream), "upload uniform");
+    fio.n_cand = g->d_ncand;
+    fio.cand_ld = vocab;
+    fio.cand_ids = g->d_cids;
+    fio.cand_vals = g->d_cvals;
+    fio.keep = g->d_keep;
+    fio.uniforms = g->d_u;
+    fio.out_token = g->d_tok;
+    LAL__CHECK(lal_gpu_sample_finish(g->ctx, 1, vocab, p, &fio, g->stream), "lal_gpu_sample_finish");
+    int tok = 0;
+    LAL__CHECK(lal_gpu_memcpy_d2h(&tok, g->d_tok, sizeof tok, g->stream), "download token");
+    if (tok < 0) lal__die("lal_gpu_sample_finish (pool above its buffer)", LAL_GPU_E_RANGE);
     return tok;
 }
 
@@ -223,7 +271,7 @@ static int lal__prepare(int vocab, int top_k, const int *recent, int *n_recent)
 {
     if (!recent || *n_recent < 0) *n_recent = 0;
     if (*n_recent > LAL_GPU_MAX_HISTORY) lal__die("history longer than LAL_GPU_MAX_HISTORY", LAL_GPU_E_RANGE);
-    if (top_k > LAL_GPU_MAX_K && top_k <= vocab)
+    if ((top_k < vocab ? top_k : vocab) > LAL_GPU_MAX_K)
         lal__die("top_k above LAL_GPU_MAX_K", LAL_GPU_E_RANGE);
     if (vocab <= 0) return 0;
     lal__ensure(vocab);
@@ -368,13 +416,14 @@ static int lal__sample_common(float *logits, int vocab_size, float temperature, 
         tok = lal__run_plugin(logits, vocab_size, &p, recent, n_recent, hv);
     } else {
         /* The filtered sampler draws only when its softmax sum is positive.
-         * Run with u = 0 first: when sum <= 0 that token (the argmax of the
-         * kept set) is final and no rand() is consumed; when the drawn u is
-         * 0 it is final as well; otherwise run again with u. */
-        tok = lal__run(logits, vocab_size, &p, recent, n_recent, 0.0f, &sum, hv);
+         * Run with u = 0 first, keeping the pool on the device: when sum <= 0
+         * that token (the argmax of the kept set) is final and no rand() is
+         * consumed; when the drawn u is 0 it is final as well; otherwise the
+         * draw with u runs over the pool alone. */
+        tok = lal__run_io(logits, vocab_size, &p, recent, n_recent, 0.0f, &sum, hv, 1);
         if (sum > 0.0f) {
             const float u = lal__uniform();
-            if (u != 0.0f) tok = lal__run(logits, vocab_size, &p, recent, n_recent, u, &sum, NULL);
+            if (u != 0.0f) tok = lal__draw_pool(vocab_size, &p, u);
         }
     }
     lal__write_back(logits, vocab_size, recent, n_recent, hv);
@@ -413,7 +462,8 @@ static void lal_sampling_set_filter_ops(int ban_last, int ban_repeat, const int 
     g->ban_repeat = ban_repeat;
     g->n_ban = n_ban_ids;
     if (n_ban_ids > 0) {
-        LAL__CHECK(lal_gpu_memcpy_h2d(g->d_ban, ban_ids, (size_t)n_ban_ids * sizeof(int), g->stream),
+        memcpy(g->h_ban, ban_ids, (size_t)n_ban_ids * sizeof(int));
+        LAL__CHECK(lal_gpu_memcpy_h2d(g->d_ban, g->h_ban, (size_t)n_ban_ids * sizeof(int), g->stream),
                    "upload ban ids");
         LAL__CHECK(lal_gpu_stream_sync(g->stream), "stream sync");
     }

@@ -16,7 +16,11 @@ E_INVAL, E_RANGE, E_HIP, E_NOMEM, E_NODEV = -1, -2, -3, -4, -5
 VARIANT_BASIC = 0
 VARIANT_FILTERED = 1
 F_WRITEBACK = 0x1
-F_DRAW_GPT2 = 0x2
+F_DRAW_GPT2 = 0x2       # also LAL_GPU_F_DRAW_ALL_IDS
+F_DRAW_ALL_IDS = F_DRAW_GPT2
+F_FALLBACK_ZERO = 0x4
+F_GREEDY_FILTER = 0x8
+ABI_VERSION = 3
 MAX_K = 512
 MAX_HISTORY = 512
 MAX_BAN_IDS = 64
@@ -46,7 +50,7 @@ class SampleIO(C.Structure):
                 ("out_n_kept", C.c_void_p), ("out_sum", C.c_void_p),
                 ("cand_ld", C.c_int), ("cand_ids", C.c_void_p), ("cand_probs", C.c_void_p),
                 ("cand_kept", C.c_void_p), ("out_history_vals", C.c_void_p),
-                ("cand_vals", C.c_void_p)]
+                ("cand_vals", C.c_void_p), ("last_tokens", C.c_void_p)]
 
 
 class Gpq8Tensor(C.Structure):
@@ -128,6 +132,9 @@ def load(path=LIB_PATH):
         fn = getattr(lib, name)
         fn.restype = res
         fn.argtypes = args
+    if lib.lal_gpu_abi_version() != ABI_VERSION:
+        raise GpuError(f"{path}: ABI version {lib.lal_gpu_abi_version()}, this binding is {ABI_VERSION}; "
+                       "rebuild the library")
     _LIB = lib
     return lib
 

@@ -3,7 +3,10 @@
 Invoked by __graft_entry__.build(); compiles in-tree so the shared objects
 travel with the source tree.
 """
+import hashlib
+import json
 import os
+import re
 import subprocess
 import sys
 
@@ -25,12 +28,54 @@ def run(cmd, **kw):
     subprocess.check_call(cmd, **kw)
 
 
+RESOURCES = os.path.join(HERE, "kernel_resources.json")
+KERNEL_SRC = os.path.join(HERE, "csrc", "lal_gpu_sample.hip")
+
+
+def source_digest():
+    """sha256 of the kernel source and the headers it includes."""
+    h = hashlib.sha256()
+    for p in [KERNEL_SRC] + sorted(os.path.join(ROOT, "include", f) for f in os.listdir(os.path.join(ROOT, "include"))):
+        with open(p, "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()
+
+
+def parse_resource_remarks(text):
+    """Per-kernel register, scratch, occupancy and LDS figures from the
+    compiler's -Rpass-analysis=kernel-resource-usage remarks."""
+    kernels, cur = {}, None
+    for line in text.splitlines():
+        m = re.search(r"Function Name: (\S+)", line)
+        if m:
+            cur = kernels.setdefault(m.group(1), {})
+            continue
+        m = re.search(r"(VGPRs|AGPRs|SGPRs|ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]|"
+                      r"LDS Size \[bytes/block\]): (\d+)", line)
+        if m and cur is not None:
+            cur[m.group(1).split()[0]] = int(m.group(2))
+    return kernels
+
+
 def build_gpu_lib():
-    srcs = [os.path.join(HERE, "csrc", "lal_gpu_sample.hip"), os.path.join(HERE, "csrc", "lal_gpq8.cpp")]
+    srcs = [KERNEL_SRC, os.path.join(HERE, "csrc", "lal_gpq8.cpp")]
     out = os.path.join(HERE, "liblal_gpu.so")
     tmp = out + ".tmp"
-    run([HIPCC] + HIP_FLAGS + ["-o", tmp] + srcs)
+    cmd = [HIPCC] + HIP_FLAGS + ["-Rpass-analysis=kernel-resource-usage", "-o", tmp] + srcs
+    print("+", " ".join(cmd), flush=True)
+    proc = subprocess.run(cmd, stderr=subprocess.PIPE, text=True)
+    remarks = proc.stderr
+    # the remarks are for the resource report; anything else is shown
+    other = [l for l in remarks.splitlines()
+             if "kernel-resource-usage" not in l and not re.match(r"^\s*\d*\s*\|", l)]
+    if other:
+        print("\n".join(other), file=sys.stderr)
+    if proc.returncode != 0:
+        raise subprocess.CalledProcessError(proc.returncode, cmd)
     os.replace(tmp, out)
+    with open(RESOURCES, "w") as f:
+        json.dump({"source_sha256": source_digest(), "kernels": parse_resource_remarks(remarks)}, f,
+                  indent=1, sort_keys=True)
     return out
 
 

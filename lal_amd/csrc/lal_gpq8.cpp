@@ -54,6 +54,9 @@ int parse(lal_gpq8_file *f)
     int32_t n = 0;
     if (!c.take(magic, 4) || memcmp(magic, "GPQ8", 4) != 0) return LAL_GPU_E_INVAL;
     if (!c.take(&n, 4) || n < 0) return LAL_GPU_E_INVAL;
+    // every record holds at least 21 bytes (key length, ndim, qtype, data
+    // length, scale count), so a count the file cannot hold is malformed
+    if ((uint64_t)n > (uint64_t)(c.end - c.p) / 21u) return LAL_GPU_E_INVAL;
     f->keys.reserve((size_t)n);
     f->tensors.reserve((size_t)n);
     for (int32_t i = 0; i < n; i++) {
@@ -121,7 +124,14 @@ int lal_gpq8_open(const char *path, lal_gpq8_file **out)
         return LAL_GPU_E_NOMEM;
     }
     madvise(f->base, f->size, MADV_SEQUENTIAL);
-    const int rc = parse(f);
+    int rc;
+    try {
+        rc = parse(f);
+    } catch (const std::bad_alloc &) {
+        rc = LAL_GPU_E_NOMEM;
+    } catch (...) {
+        rc = LAL_GPU_E_INVAL;
+    }
     if (rc != LAL_GPU_OK) {
         lal_gpq8_close(f);
         return rc;

@@ -244,6 +244,7 @@ struct Smem {
     int wcnt[NWAVE];      // entries in each wave buffer (dead ones are nan)
     int walive[NWAVE];    // live entries
     unsigned tau_key;     // max over the waves' thresholds (order-preserving key)
+    int nan_flag;         // the row holds a nan processed value
     float wtau[NWAVE];
     int wstrict[NWAVE];
     int wsum[2][NWAVE];
@@ -282,12 +283,14 @@ struct KArgs {
     float *out_hvals;
     const int *ban_ids;
     int n_ban;
+    const int *last_tokens;  // [batch] id ban_last drops (NULL: history[len-1])
     float T, top_p, pen;
     int k;
     int variant;
     unsigned flags;
     int ban_last, ban_repeat, mask_recent;
     int greedy;     // greedy path: k = 1, first index among the maxima
+    int fallback;   // token when no running sum reaches r: V-1, or 0 (F_FALLBACK_ZERO)
     int apply_pen;  // penalty applied for this variant / greedy state
     int any_bans;
     // slicing: each row is split into nslice contiguous slices, one workgroup
@@ -401,9 +404,11 @@ __device__ __forceinline__ bool allow_bit(const uint32_t *row_bits, int e)
 }
 
 // repetition penalty applied `count` times: x>0 ? x/p : x*p
-// (runtime/lal_sampling.h:63-64, once per history occurrence)
+// (runtime/lal_sampling.h:63-64, once per history occurrence).  A nan stays
+// the same nan, bit for bit, as the x86 multiply returns it.
 __device__ __forceinline__ float penalise(float x, int count, float pen)
 {
+    if (x != x) return x;
     for (int c = 0; c < count; ++c) x = (x > 0.0f) ? x / pen : x * pen;
     return x;
 }
@@ -739,16 +744,27 @@ __device__ __forceinline__ int wave_append(float *bv, int *bi, int base, const f
 // Offer this wave's values to its buffer: x[i] are upper bounds of the
 // processed logits (nan when out of range), tcmp the current filter.  On
 // overflow the wave resolves exact values (into a separate array), raises tau
-// to the k-th largest of buffer + offered values and compacts.
+// to the k-th largest of buffer + offered values and compacts.  Element
+// e = eb[i/4] + i%4 is part of the row when 0 <= e < elim; a nan bound there
+// is a nan in the row and raises *nan_flag (padding lanes are nan as well).
 // Wave-synchronous, no workgroup barrier.
 template <int NQ, int CAPW>
 __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, const RowCtx &R,
                                            const float (&x)[4 * NQ],
-                                           const int (&eb)[NQ], float tcmp, WState &st, int k,
-                                           unsigned *tau_key_shared)
+                                           const int (&eb)[NQ], int elim, float tcmp, WState &st, int k,
+                                           unsigned *tau_key_shared, int *nan_flag)
 {
     constexpr int NV = 4 * NQ;
     const int tag = R.use_hash ? UNREFINED : 0;
+    {
+        bool nan_here = false;
+#pragma unroll
+        for (int i = 0; i < NV; ++i) {
+            const int e = eb[i >> 2] + (i & 3);
+            nan_here |= (x[i] != x[i]) && e >= 0 && e < elim;
+        }
+        if (__ballot(nan_here) && lane_id() == 0) *nan_flag = 1;
+    }
     // append path: the per-slot ballots give the count (scalar popcounts) and
     // each lane's position (mbcnt); no cross-lane data exchange
     int total = 0;
@@ -792,10 +808,21 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
     float tk = st.tau;
     bool strict = st.strict;
     if (cnt + offered > CAPW) {
+        // count of buffer + offered values >= t
+        auto count_ge = [&](float t) {
+            int nge = 0;
+            for (int j = lane_id(); j < cnt; j += 64) nge += (bv[j] >= t);
+#pragma unroll
+            for (int i = 0; i < NV; ++i) nge += ((m >> i) & 1u) && (y[i] >= t);
+            return wave_sum(nge);
+        };
+        int nge = CAPW + 1;
         if (k <= 64) {
-            // the k-th largest of the lanes' maxima: k distinct values of the
-            // set, so no larger than its k-th largest (a valid, cheap bound;
-            // every lane holds at least CAPW/64 values here)
+            // The k-th largest of the lanes' maxima: k distinct values of the
+            // set reach it, so it is no larger than the set's k-th largest (a
+            // valid, cheap bound).  Used only when it leaves at most CAPW
+            // values: strictly above it there can be more than CAPW (up to k-1
+            // lanes' worth), and a lane without values makes it key 0.
             uint32_t mk = 0u;
 #pragma unroll
             for (int i = 0; i < NV; ++i)
@@ -804,15 +831,18 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
                 const float v = bv[j];
                 if (v == v) mk = max(mk, fkey(v));
             }
-            tk = keyf(wave_kth_lane_key(mk, k));
-        } else {
-            tk = keyf(wave_kth_key<NV>(hist, bv, cnt, y, m, k));
+            const uint32_t K = wave_kth_lane_key(mk, k);
+            if (K != 0u) {
+                tk = keyf(K);
+                nge = count_ge(tk);
+            }
         }
-        int nge = 0;
-        for (int j = lane_id(); j < cnt; j += 64) nge += (bv[j] >= tk);
-#pragma unroll
-        for (int i = 0; i < NV; ++i) nge += ((m >> i) & 1u) && (y[i] >= tk);
-        strict = wave_sum(nge) > CAPW;
+        if (nge > CAPW) {
+            // the exact k-th largest: fewer than k <= CAPW values lie above it
+            tk = keyf(wave_kth_key<NV>(hist, bv, cnt, y, m, k));
+            nge = count_ge(tk);
+        }
+        strict = nge > CAPW;
         cnt = wave_compact(bv, bi, cnt, tk, strict);
     }
     st.cnt = wave_append<NQ>(bv, bi, cnt, y, eb, m, tk, strict, 0);
@@ -1103,6 +1133,97 @@ __device__ __forceinline__ float rescan_sequential(const KArgs &A, SM &S, const 
     }
     if (token) *token = found;
     return acc;
+}
+
+// Threshold of a row that holds nan values: the size-k min-heap of
+// runtime/lal_sampling.h:69-104 (tools/server/qwen7b_server.c:238-256)
+// replayed over the processed row in id order.  A nan never passes the heap's
+// comparisons, so it rises to the root while the heap fills, sinks below
+// values pushed after it and is never replaced; the root at the end is the
+// threshold (nan when a nan is the root).  Wave 0 runs the replay: 16 chunks of
+// 64 values are loaded at a time and staged in LDS; in a chunk, the first value
+// that acts on the heap (any while it fills, then one above the root) is
+// applied by lane 0, the root is re-read and the rest of the chunk filtered
+// again.  The heap lives in S.cval and the staged values in S.cidx (the
+// candidate buffers are not used on this path).
+template <bool HAS_BIAS, bool HAS_ALLOW, class SM>
+__device__ __forceinline__ float heap_replay_threshold(const KArgs &A, SM &S, const RowCtx &R, int k)
+{
+    constexpr int NB = 16;
+    static_assert(sizeof(S.cidx) >= 64 * NB * sizeof(float), "staging area");
+    float *hv = S.cval;
+    float *stage = reinterpret_cast<float *>(S.cidx);
+    __syncthreads();
+    if (wave_id() == 0) {
+        const int lane = lane_id();
+        int size = 0;
+        for (int base = 0; base < A.V; base += 64 * NB) {
+            float xr[NB];
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int e = base + 64 * j + lane;
+                xr[j] = (e < A.V) ? R.row[e] : 0.0f;
+            }
+#pragma unroll
+            for (int j = 0; j < NB; ++j) {
+                const int e = base + 64 * j + lane;
+                if (e < A.V)
+                    stage[64 * j + lane] =
+                        exact_value(R, e, upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, R.abits, e, xr[j]));
+            }
+            wave_sync();
+            const int nch = min(NB, (A.V - base + 63) >> 6);
+            for (int j = 0; j < nch; ++j) {
+                const int c0 = base + 64 * j;
+                const float x = (c0 + lane < A.V) ? stage[64 * j + lane] : 0.0f;
+                unsigned long long todo = __ballot(c0 + lane < A.V);
+                while (todo) {
+                    const float root = hv[0];
+                    const unsigned long long m = __ballot(size < k || x > root) & todo;
+                    if (!m) break;
+                    const int l = (int)__builtin_ctzll(m);
+                    const float val = readlane_f(x, l);
+                    if (lane == 0) {
+                        if (size < k) {
+                            int c = size;
+                            hv[c] = val;
+                            while (c > 0) {
+                                const int p = (c - 1) >> 1;
+                                if (hv[p] <= hv[c]) break;
+                                const float t = hv[p];
+                                hv[p] = hv[c];
+                                hv[c] = t;
+                                c = p;
+                            }
+                        } else {
+                            hv[0] = val;
+                            int p = 0;
+                            for (;;) {
+                                const int lc = 2 * p + 1, rc = 2 * p + 2;
+                                int sm = p;
+                                if (lc < size && hv[lc] < hv[sm]) sm = lc;
+                                if (rc < size && hv[rc] < hv[sm]) sm = rc;
+                                if (sm == p) break;
+                                const float t = hv[p];
+                                hv[p] = hv[sm];
+                                hv[sm] = t;
+                                p = sm;
+                            }
+                        }
+                    }
+                    if (size < k) ++size;
+                    wave_sync();
+                    todo &= (l == 63) ? 0ull : (~0ull << (l + 1));
+                }
+            }
+            wave_sync();  // the staged chunk is read before the next one is written
+        }
+        if (lane == 0) S.redf[0] = hv[0];
+    }
+    __syncthreads();
+    const float T = S.redf[0];
+    __syncthreads();
+    return T;
 }
 
 // Candidate outputs for a rescanned row: the first cand_ld pool ids in id
@@ -1426,7 +1547,7 @@ __device__ __forceinline__ RowResult wave_epilogue(const KArgs &A, SM &S, int nc
             } else {
                 f = seq_first_reach(buf, nc, r);
             }
-            res.token = (f < nc) ? readlane_i(id, f) : A.V - 1;
+            res.token = (f < nc) ? readlane_i(id, f) : A.fallback;
         }
     }
     if (valid && lane < A.cand_ld) {
@@ -1553,7 +1674,7 @@ __device__ __forceinline__ RowResult block_epilogue(const KArgs &A, SM &S, int n
             for (int r = 0; r < PER; ++r)
                 if (kept[r] && rr <= ep[tid + r * WG]) cand = min(cand, tid + r * WG);
             const int j = block_min(S, cand);
-            res.token = (j == INT_MAX) ? A.V - 1 : S.cidx[j];
+            res.token = (j == INT_MAX) ? A.fallback : S.cidx[j];
         }
     }
     if (A.cand_ld > 0) {
@@ -1616,7 +1737,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     const int h0 = (tid < nh) ? hrow[tid] : -1;
     const int h1 = (tid + WG < nh) ? hrow[tid + WG] : -1;
     const int bid = (tid < A.n_ban) ? A.ban_ids[tid] : -1;
-    const float uu = (A.uniforms && !A.greedy) ? A.uniforms[b] : 0.0f;
+    const int last_tok = (A.last_tokens && A.ban_last) ? A.last_tokens[b] : -1;
     const uint64_t xtab = (tid < 32) ? kExp2Tab[tid] : 0ull;
 
     const RowGeo g = row_geo(row, V);
@@ -1700,6 +1821,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         S.hinfo[s] = 0;
     }
     if (tid < 32) S.exptab[tid] = xtab;
+    if (tid == 0) S.nan_flag = 0;
     __syncthreads();
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
@@ -1708,11 +1830,12 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         if (i >= nh || t < 0 || t >= V) continue;
         int flags = 0;
         if (A.mask_recent > 0 && i >= nh - A.mask_recent) flags |= HF_MASKPRE;
-        if (A.ban_last && i == nh - 1) flags |= HF_BAN;
+        if (A.ban_last && !A.last_tokens && i == nh - 1) flags |= HF_BAN;
         if (A.ban_repeat > 0 && i >= nh - A.ban_repeat) flags |= HF_BAN;
         hash_insert(S.hkey, S.hinfo, t, A.apply_pen ? 1 : 0, flags);
     }
     if (bid >= 0 && bid < V) hash_insert(S.hkey, S.hinfo, bid, 0, HF_BAN);
+    if (tid == 0 && last_tok >= 0 && last_tok < V) hash_insert(S.hkey, S.hinfo, last_tok, 0, HF_BAN);
     if (use_est && w == 0) {
         // the ks-th largest of the 256 keys, bit by bit (ballot counts)
         const uint32_t k0 = skeys[lane], k1 = skeys[64 + lane], k2 = skeys[128 + lane],
@@ -1751,12 +1874,17 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     WState st;
     for (int attempt = 0; attempt < 2; ++attempt) {
         if (attempt == 1) {
-            // the estimate was above the row's k-th largest: stream again
+            // the estimate was above the row's k-th largest: stream again.  The
+            // share's start goes through an opaque copy, so that the compiler
+            // recomputes these loads' masks and addresses here instead of
+            // holding the first pass's across the whole stream.
+            int qa = __builtin_amdgcn_readfirstlane(qb);
+            asm volatile("" : "+s"(qa));
 #pragma unroll
             for (int u = 0; u < U4; ++u) {
-                const int q = qb + u * 64 + lane;
+                const int q = qa + u * 64 + lane;
                 cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
-                const int q1 = qb + WITER + u * 64 + lane;
+                const int q1 = qa + WITER + u * 64 + lane;
                 nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
             }
         }
@@ -1774,7 +1902,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         float x[4] = {NAN, NAN, NAN, NAN};
         const int eb[1] = {e};
         if (e >= 0) x[0] = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
-        wave_offer<1, CAPW>(bv, bi, hist, R, x, eb, -INFINITY, st, k, &S.tau_key);
+        wave_offer<1, CAPW>(bv, bi, hist, R, x, eb, (e >= 0) ? e + 1 : 0, -INFINITY, st, k, &S.tau_key,
+                            &S.nan_flag);
     }
     for (int q0 = qb; q0 < qe; q0 += WITER) {
         // two iterations stay in flight while this one is filtered
@@ -1835,14 +1964,17 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 #pragma unroll
                     for (int c = 0; c < 4; ++c) x[4 * u + c] = NAN;
         }
+        // a value enters the offer when it passes the filter or is nan (a nan
+        // in the row, or a padding lane of a partial iteration)
         unsigned long long any = 0ull;
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) any |= __ballot(x[i] >= tcmp);
+        for (int i = 0; i < VPL; ++i) any |= __ballot(!(x[i] < tcmp));
         if (any) {
             int eb[U4];
 #pragma unroll
             for (int u = 0; u < U4; ++u) eb[u] = g.head + 4 * (q0 + u * 64 + lane);
-            wave_offer<U4, CAPW>(bv, bi, hist, R, x, eb, tcmp, st, k, &S.tau_key);
+            wave_offer<U4, CAPW>(bv, bi, hist, R, x, eb, g.head + 4 * qe, tcmp, st, k, &S.tau_key,
+                                 &S.nan_flag);
         }
 #pragma unroll
         for (int u = 0; u < U4; ++u) {
@@ -1882,10 +2014,20 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             tot += S.walive[ww];
             strict_any |= S.wstrict[ww];
         }
-        if (tau_est == -INFINITY || strict_any || tot >= k) break;
+        if (tau_est == -INFINITY || strict_any || tot >= k || S.nan_flag) break;
         tau_est = -INFINITY;
     }
     }  // attempt
+
+    // Past the stream.  The arguments are read again from the kernel argument
+    // segment through an opaque pointer, so that the fields the rest of the
+    // row needs (outputs, epilogue parameters, slice lists) are loaded here
+    // instead of being held in scalar registers across the stream loop.
+    {
+    typedef __attribute__((address_space(4))) const KArgs *KArgsConst;
+    KArgsConst kargs = (KArgsConst)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(kargs));
+    const KArgs &A = *(const KArgs *)kargs;
 
     if (nsl > 1) {
         // ---- slice: publish the values that can reach the row's pool -------
@@ -2008,7 +2150,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             dev_store(m + 0, overflow ? 0 : n_s);
             dev_store(m + 1, (int)__float_as_uint(ltau));
             dev_store(m + 2, lstrict ? 1 : 0);
-            dev_store(m + 3, overflow ? 1 : 0);
+            dev_store(m + 3, (overflow ? 1 : 0) | (S.nan_flag ? 2 : 0));
         }
         wait_stores_done();
         __syncthreads();
@@ -2039,13 +2181,21 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
                 mstr[lane] = st;
             }
             if (lane == 63) offs[MAX_SLICES] = incl;
-            const bool any_ov = __ballot(ov != 0) != 0ull;
-            if (lane == 0) offs[MAX_SLICES + 1] = any_ov ? 1 : 0;
+            const bool any_ov = __ballot(ov & 1) != 0ull;
+            const bool any_nan = __ballot(ov & 2) != 0ull;
+            if (lane == 0) {
+                offs[MAX_SLICES + 1] = any_ov ? 1 : 0;
+                S.nan_flag = any_nan ? 1 : 0;
+            }
         }
         __syncthreads();
         const int ntot = offs[MAX_SLICES];
         if (offs[MAX_SLICES + 1]) {
-            // a slice list did not fit: report the row as unsampled
+            // A slice list did not fit.  Unreachable: a list holds either
+            // values >= a slice's k-th largest when they fit, or values strictly
+            // above it (or above a wave's tie threshold t* >= it), of which
+            // there are fewer than k, and the host keeps lcap > k.  Reported as
+            // token -1 (documented as an internal error) rather than sampled.
             if (tid == 0) {
                 A.out_token[b] = -1;
                 if (A.out_ncand) A.out_ncand[b] = -1;
@@ -2108,7 +2258,26 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     float T = -INFINITY;
     bool rescan = false;
     int nc = 0, off = 0;
-    if (total >= k) {
+    int forced_token = -1;
+    const bool nan_row = S.nan_flag != 0;
+    bool nan_first = false;
+    if (nan_row && A.greedy) {
+        const float y0 = rescan_value<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, 0);
+        nan_first = y0 != y0;
+    }
+    if (nan_row && !A.greedy) {
+        // A nan compares false with everything, so the reference heap's
+        // threshold depends on where the nan entered it: replay the heap
+        T = heap_replay_threshold<HAS_BIAS, HAS_ALLOW>(A, S, R, k);
+        rescan = true;
+    } else if (nan_first) {
+        // the greedy scan (best = 0; later ids win only when strictly larger)
+        // keeps id 0 when its value is nan; otherwise nan never wins and the
+        // k = 1 selection below is exact
+        T = NAN;
+        forced_token = 0;
+        rescan = true;
+    } else if (total >= k) {
         uint32_t kn, kx;
         block_key_range(S, kn, kx);
         T = keyf(block_kth_union<CAPW>(S, k, kn, kx));
@@ -2122,6 +2291,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
 
     const bool top_p_on = (A.top_p > 0.0f && A.top_p < 1.0f) && !A.greedy;
+    // the row's uniform, read only now that the stream's registers are free
+    const float uu = (A.uniforms && !A.greedy) ? A.uniforms[b] : 0.0f;
     int token = V - 1;
     int n_cand = 0, n_kept = 0;
     float sum2 = 0.0f;
@@ -2203,17 +2374,21 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         }
 
         if (nc == 0) {
-            token = V - 1;
+            // no value reaches the threshold: the softmax sum is 0, so the
+            // filtered variant's argmax over nothing gives 0, the draw r = 0
+            token = (A.variant == LAL_GPU_VARIANT_FILTERED || (A.flags & LAL_GPU_F_DRAW_GPT2)) ? 0 : A.fallback;
         } else if (A.greedy) {
             if (nc <= 64) __syncthreads();  // wave 0 sorted the pool
             token = S.cidx[0];
+            if ((A.flags & LAL_GPU_F_GREEDY_FILTER) && is_banned(S, 0)) token = 0;
             n_kept = 1;
             for (int j = tid; j < nc && j < A.cand_ld; j += WG) {
                 const size_t o = (size_t)b * A.cand_ld + j;
+                const bool kept = S.cidx[j] == token;
                 if (A.cand_ids) A.cand_ids[o] = S.cidx[j];
                 if (A.cand_vals) A.cand_vals[o] = S.cval[j];
-                if (A.cand_kept) A.cand_kept[o] = (j == 0);
-                if (A.cand_probs) A.cand_probs[o] = (j == 0) ? 1.0f : 0.0f;
+                if (A.cand_kept) A.cand_kept[o] = kept ? 1 : 0;
+                if (A.cand_probs) A.cand_probs[o] = kept ? 1.0f : 0.0f;
             }
         } else if (nc <= 64) {
             if (w == 0) {
@@ -2251,7 +2426,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         n_cand = rs.n_cand;
         n_kept = rs.n_kept;
         if (A.greedy) {
-            token = rs.first_kept;
+            token = (forced_token >= 0) ? forced_token : rs.first_kept;
+            if ((A.flags & LAL_GPU_F_GREEDY_FILTER) && is_banned(S, 0)) token = 0;
             n_kept = 1;
             if (A.cand_ld > 0)
                 rescan_write_cands<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, false, N, 0.0f,
@@ -2270,7 +2446,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
                     int f = -1;
                     rescan_sequential<HAS_BIAS, HAS_ALLOW>(A, S, row, abits, use_hash, T, use_ban, N,
                                                            mx, true, rr, &f);
-                    token = (f < 0) ? V - 1 : f;
+                    token = (f < 0) ? A.fallback : f;
                 }
             }
             if (A.cand_ld > 0)
@@ -2309,6 +2485,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             }
         }
     }
+    }  // arguments read again
 }
 
 // ---------------------------------------------------------------------------
@@ -2390,7 +2567,7 @@ __global__ __launch_bounds__(WG) void finish_rows_kernel(FinishArgs F)
         acc = block_seq_prefix(S, S.ep, m, acc);
     }
     const float sum = acc;
-    int token = F.V - 1;
+    int token = (F.flags & LAL_GPU_F_FALLBACK_ZERO) ? 0 : F.V - 1;
     if (F.variant == LAL_GPU_VARIANT_FILTERED && sum <= 0.0f) {
         // first id of the largest kept value above -1e30 (ids of entries
         // outside the pool need not be in order)
@@ -3511,6 +3688,11 @@ struct lal_gpu_ctx {
     int max_batch;
     int max_vocab;
     int ncu;  // compute units
+    int forced_slices;  // LAL_GPU_SLICES at creation (0: choose per call)
+    // LM head tuning overrides read at creation (0 / -1: the measured defaults)
+    int lmh_wg;         // LAL_GPU_LMH_WG: workgroups per CU
+    int lmh_xres;       // LAL_GPU_LMH_XRES: 0 disables the resident-activation kernel
+    int lmh_pd;         // LAL_GPU_LMH_PD: W steps in flight (2 or 3)
     // slice lists (see KArgs): max_batch x FLAT_MAX entries, metadata for up
     // to MAX_SLICES slices per row, one arrival counter per row (zeroed here,
     // reset by every row's finisher)
@@ -3585,6 +3767,11 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
             ncu = 256;
         c->ncu = ncu;
     }
+    if (const char *env = getenv("LAL_GPU_SLICES")) c->forced_slices = std::max(0, atoi(env));
+    c->lmh_xres = -1;
+    if (const char *env = getenv("LAL_GPU_LMH_WG")) c->lmh_wg = std::max(0, atoi(env));
+    if (const char *env = getenv("LAL_GPU_LMH_XRES")) c->lmh_xres = atoi(env) != 0;
+    if (const char *env = getenv("LAL_GPU_LMH_PD")) c->lmh_pd = (atoi(env) == 3) ? 3 : 2;
     const size_t nl = (size_t)max_batch * FLAT_MAX;
     hipError_t e = hipMalloc((void **)&c->lst_val, nl * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->lst_idx, nl * sizeof(int));
@@ -3619,12 +3806,9 @@ void lal_gpu_destroy(lal_gpu_ctx *ctx)
 // (about one per slot: 4 per CU): slices of at least 64 Ki elements, 32 Ki
 // for at most 128 rows, 16 Ki for at most 16 rows; list capacity above k.
 constexpr int TARGET_WGS = 1024;
-static int choose_slices(int batch, int vocab, int k_eff, int flat)
+static int choose_slices(int batch, int vocab, int k_eff, int flat, int forced)
 {
-    if (const char *env = getenv("LAL_GPU_SLICES")) {
-        const int n = atoi(env);
-        if (n >= 1) return std::min(std::min(n, MAX_SLICES), std::max(1, flat / (k_eff + 1)));
-    }
+    if (forced >= 1) return std::min(std::min(forced, MAX_SLICES), std::max(1, flat / (k_eff + 1)));
     const int min_len = (batch <= 16) ? 16384 : (batch <= 128) ? 32768 : 65536;
     int n = (TARGET_WGS + batch - 1) / batch;
     n = std::min(n, std::max(1, vocab / min_len));
@@ -3640,7 +3824,9 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     if (batch > ctx->max_batch || vocab > ctx->max_vocab) return LAL_GPU_E_RANGE;
     if (!io->logits || !io->out_token || io->ld < vocab) return LAL_GPU_E_INVAL;
     const bool greedy = !(p->temperature > 0.0f) || p->top_k <= 0;
-    if (!greedy && p->top_k > LAL_GPU_MAX_K) return LAL_GPU_E_RANGE;
+    // top_k is clamped to the vocabulary first, as the kernel and the
+    // reference (qwen7b_server.c:236) do
+    if (!greedy && std::min(p->top_k, vocab) > LAL_GPU_MAX_K) return LAL_GPU_E_RANGE;
     if (!greedy && !io->uniforms) return LAL_GPU_E_INVAL;
     if (io->history && (io->history_ld <= 0 || io->history_ld > LAL_GPU_MAX_HISTORY))
         return io->history_ld > LAL_GPU_MAX_HISTORY ? LAL_GPU_E_RANGE : LAL_GPU_E_INVAL;
@@ -3680,6 +3866,7 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     A.out_hvals = io->out_history_vals;
     A.ban_ids = p->ban_ids;
     A.n_ban = p->n_ban_ids;
+    A.last_tokens = io->last_tokens;
     A.T = p->temperature;
     A.top_p = p->top_p;
     A.pen = p->rep_penalty;
@@ -3690,29 +3877,39 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     A.ban_repeat = p->ban_repeat;
     A.mask_recent = p->mask_recent;
     A.greedy = greedy ? 1 : 0;
+    A.fallback = (p->flags & LAL_GPU_F_FALLBACK_ZERO) ? 0 : vocab - 1;
     const bool has_hist = io->history != nullptr;
     A.apply_pen = (p->rep_penalty > 1.0f && has_hist &&
                    (p->variant == LAL_GPU_VARIANT_FILTERED || !greedy)) ? 1 : 0;
-    A.any_bans = (!greedy && ((has_hist && (p->ban_last || p->ban_repeat > 0)) || p->n_ban_ids > 0)) ? 1 : 0;
+    // bans act on the pool; on greedy rows only with F_GREEDY_FILTER
+    const bool bans_apply = !greedy || (p->flags & LAL_GPU_F_GREEDY_FILTER);
+    const bool has_last = has_hist || io->last_tokens;
+    A.any_bans = (bans_apply && ((has_last && p->ban_last) || (has_hist && p->ban_repeat > 0) ||
+                                 p->n_ban_ids > 0)) ? 1 : 0;
     if (!has_hist) {
-        A.ban_last = 0;
         A.ban_repeat = 0;
         A.mask_recent = 0;
     }
+    if (!has_last) A.ban_last = 0;
     if (!A.any_bans) {
         A.ban_last = 0;
         A.ban_repeat = 0;
         A.n_ban = 0;
+        A.last_tokens = nullptr;
     }
 
     hipStream_t s = (hipStream_t)stream;
-    const bool small = greedy || p->top_k <= K_SMALL_MAX;
     const int k_eff = greedy ? 1 : std::min(p->top_k, vocab);
+    const bool small = k_eff <= K_SMALL_MAX;
     const int flat = NWAVE * (small ? CAPW_SMALL : CAPW_LARGE);
     A.batch = batch;
-    A.nslice = choose_slices(batch, vocab, k_eff, flat);
+    A.nslice = choose_slices(batch, vocab, k_eff, flat, ctx->forced_slices);
     A.ncu = ctx->ncu;
     A.lcap = flat / A.nslice;
+    // a slice list must hold more than k values (see the finisher): always
+    // true by choose_slices, checked so that the kernel's overflow branch
+    // stays unreachable
+    if (A.nslice > 1 && A.lcap <= k_eff) return LAL_GPU_E_RANGE;
     A.lst_val = ctx->lst_val;
     A.lst_idx = ctx->lst_idx;
     A.lst_meta = ctx->lst_meta;
@@ -3789,7 +3986,7 @@ int lal_gpu_lm_head_q8(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx, 
     }
     if (batch > LMH_MAXB) {
         int per_cu = 4;
-        if (const char *env = getenv("LAL_GPU_LMH_WG")) per_cu = std::max(1, atoi(env));
+        if (ctx->lmh_wg > 0) per_cu = ctx->lmh_wg;
         const unsigned nwg = (unsigned)std::min(per_cu * ctx->ncu, (vocab + LMM_TILE_V - 1) / LMM_TILE_V);
         for (int b0 = 0; b0 < batch; b0 += LMM_MAXB) {
             const int nb = std::min(LMM_MAXB, batch - b0);
@@ -3875,9 +4072,9 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
         const int mt = (nb + 15) / 16;
         // up to 16 rows: the activations resident in LDS (64 KB: 2 workgroups per CU)
         bool xres = mt == 1 && n <= LMX_MAXN;
-        if (const char *env = getenv("LAL_GPU_LMH_XRES")) xres = xres && atoi(env) != 0;
+        if (ctx->lmh_xres == 0) xres = false;
         int per_cu = xres ? 2 : (mt <= 2) ? 4 : 2;  // workgroups per CU (measured best at each shape)
-        if (const char *env = getenv("LAL_GPU_LMH_WG")) per_cu = std::max(1, atoi(env));
+        if (ctx->lmh_wg > 0) per_cu = ctx->lmh_wg;
         const unsigned nwg = (unsigned)std::max(1, std::min(per_cu * ctx->ncu, (ntile + LMM_WAVES - 1) / LMM_WAVES));
         const dim3 g2(nwg), blk(64 * LMM_WAVES);
         if (xres) {
@@ -3887,7 +4084,7 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
             continue;
         }
         int pd = (mt <= 2) ? 2 : 3;  // W steps in flight per wave
-        if (const char *env = getenv("LAL_GPU_LMH_PD")) pd = (atoi(env) == 3) ? 3 : 2;
+        if (ctx->lmh_pd) pd = ctx->lmh_pd;
 #define LAL_LMH(M, D) \
     hipLaunchKernelGGL((lm_head_packed_kernel<M, D>), g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb)
         switch (mt * 4 + pd) {

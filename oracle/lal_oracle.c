@@ -150,8 +150,32 @@ int lal_oracle_sample_row(float *row, int V, const lal_oracle_params *p,
 
     if (greedy) {
         token = argmax_first(y, V);
-        inf.greedy = 1;
+        /* the selection's threshold and pool: the argmax value */
         inf.threshold = y[token];
+        if (p->flags & LAL_ORACLE_F_GREEDY_FILTER) {
+            /* mini_server.c:284-288 hands &km (km = the argmax) to the filter
+             * as its keep mask: element 0 is the token id.  Only id 0 lies
+             * inside that one-element array, so a ban of id 0 clears it
+             * (token 0); the filter is called with n_vocab = 1 so that the ids
+             * it would read past the array stay out of range. */
+            int km = token;
+            const int last = p->has_last ? p->last_token : ((n_hist > 0 && hist) ? hist[n_hist - 1] : -1);
+            if (p->ban_last && last == 0) km = 0;
+            if (p->ban_repeat > 0 && hist) {
+                int s = n_hist > p->ban_repeat ? n_hist - p->ban_repeat : 0;
+                for (int i = s; i < n_hist; i++)
+                    if (hist[i] == 0) km = 0;
+            }
+            for (int i = 0; i < p->n_ban_ids; i++)
+                if (p->ban_ids[i] == 0) km = 0;
+            if (filter) {
+                int m1 = km;
+                filter(&m1, 1, last, hist, n_hist, decode);
+                km = m1;
+            }
+            token = km;
+        }
+        inf.greedy = 1;
         int n = 0;
         for (int v = 0; v < V; v++) n += (y[v] >= inf.threshold);
         inf.n_cand = n;
@@ -219,7 +243,7 @@ int lal_oracle_sample_row(float *row, int V, const lal_oracle_params *p,
      * optional plugin with the lal_filter_topk ABI, then restore-if-empty
      * (qwen7b_server.c:260-269). */
     {
-        int last = (n_hist > 0 && hist) ? hist[n_hist - 1] : -1;
+        int last = p->has_last ? p->last_token : ((n_hist > 0 && hist) ? hist[n_hist - 1] : -1);
         if (p->ban_last && last >= 0 && last < V) keep[last] = 0;
         if (p->ban_repeat > 0 && hist) {
             int s = n_hist > p->ban_repeat ? n_hist - p->ban_repeat : 0;
@@ -268,7 +292,7 @@ int lal_oracle_sample_row(float *row, int V, const lal_oracle_params *p,
     } else {
         inf.used_uniform = 1;
         float r = u * sum;
-        token = V - 1;
+        token = (p->flags & LAL_ORACLE_F_FALLBACK_ZERO) ? 0 : V - 1;
         if ((p->flags & LAL_ORACLE_F_DRAW_GPT2) && r == 0.0f) {
             token = 0;
         } else {
@@ -317,8 +341,13 @@ void lal_oracle_sample_batch(float *logits, int B, int V, int ld,
         int nh = hist ? (hist_len ? hist_len[b] : hist_ld) : 0;
         const uint32_t *al = allow ? allow + (size_t)b * allow_ld : NULL;
         size_t co = (size_t)b * (cand_ld > 0 ? cand_ld : 0);
+        lal_oracle_params pb = *p;
+        if (p->last_tokens) {
+            pb.has_last = 1;
+            pb.last_token = p->last_tokens[b];
+        }
         out_token[b] = lal_oracle_sample_row(
-            logits + (size_t)b * ld, V, p, h, nh, al, bias, uniforms[b],
+            logits + (size_t)b * ld, V, &pb, h, nh, al, bias, uniforms[b],
             NULL, NULL, &inf, cand_ld,
             cand_ids ? cand_ids + co : NULL,
             cand_probs ? cand_probs + co : NULL,

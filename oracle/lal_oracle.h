@@ -10,6 +10,9 @@
  * samaidev/lal tree):
  *   lal_oracle_sample_row   runtime/lal_sampling.h:46-125 (variant BASIC),
  *                           tools/server/qwen7b_server.c:219-295 (FILTERED),
+ *                           tools/server/qwen_server.c:418-527 (BASIC + F_DRAW_GPT2),
+ *                           tools/mini_server.c:267-363 (FILTERED + F_FALLBACK_ZERO
+ *                           + F_GREEDY_FILTER, the filter's last token given),
  *                           tools/server/gpt2_server.c:2908-2955 (top-p),
  *                           compiler/lal.py:2220-2242 (ban_last/ban_repeat/
  *                           ban_token on the top-k keep mask)
@@ -23,6 +26,8 @@
  *   top-k / softmax / draw / penalty / filtered variant / plugin bans:
  *       golden vectors written by the reference's own C code
  *       (test_oracle_golden.py) and oracle/_ref called directly;
+ *   qwen_server / mini_server flags: against those servers' samplers
+ *       compiled in oracle/_ref (test_oracle_pins.py);
  *   logit-space ops (bias, allow bitmask, mask_recent): against the
  *       reference sampler run on the op-applied row (test_oracle_pins.py);
  *   top-p nucleus: the reference has no callable entry point; pinned by its
@@ -46,7 +51,11 @@ extern "C" {
 #define LAL_ORACLE_VARIANT_BASIC    0 /* lal_sampling.h: greedy test before penalty */
 #define LAL_ORACLE_VARIANT_FILTERED 1 /* qwen7b_server.c: penalty first, k in [1,V], sum<=0 -> argmax */
 
-#define LAL_ORACLE_F_DRAW_GPT2 0x2u   /* gpt2_server.c:2997-3002: r == 0 returns token 0 */
+#define LAL_ORACLE_F_DRAW_GPT2 0x2u   /* gpt2_server.c:2997-3002, qwen_server.c:518-524: the
+                                        draw runs over every id, r == 0 returns token 0 */
+#define LAL_ORACLE_F_FALLBACK_ZERO 0x4u  /* mini_server.c:339-347: 0 when no sum reaches r */
+#define LAL_ORACLE_F_GREEDY_FILTER 0x8u  /* mini_server.c:284-288: the argmax goes through
+                                            the filter as a one-element keep mask */
 
 typedef int (*lal_oracle_decode_fn)(int token_id, char *out_buf, int max_len);
 typedef int (*lal_oracle_filter_fn)(int *keep_mask, int n_vocab, int last_token,
@@ -65,6 +74,12 @@ typedef struct {
     int n_ban_ids;      /* lal.py ban_token(id) list */
     const int *ban_ids;
     int mask_recent;    /* last n history ids -> -inf before top-k */
+    /* the filter's last token (mini_server.c:267, `last_tok`) in place of
+     * hist[n_hist-1]: has_last = 1 and last_token, or, for the batch driver,
+     * last_tokens[B] */
+    int has_last;
+    int last_token;
+    const int *last_tokens;
 } lal_oracle_params;
 
 typedef struct {

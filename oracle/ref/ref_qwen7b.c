@@ -25,3 +25,12 @@ void lal_ref_set_filter(void *fn)
 }
 
 int lal_ref_vocab_capacity(void) { return VOCAB_SIZE; }
+
+/* Install a tokenizer vocabulary (id -> vocab string) in place of
+ * load_tokenizer's, so that the server's decode_fn (qwen7b_decode_for_filter
+ * -> decode_token, qwen7b_server.c:885-888) decodes for a loaded plugin. */
+void lal_ref_qwen7b_set_vocab(char **strs, int n)
+{
+    g_vocab_str = strs;
+    g_vocab_str_n = n;
+}

@@ -35,6 +35,14 @@ class DropIn:
         L.dh_set_filter_plugin.argtypes = [C.c_void_p]
         self.plugins = {nm: C.cast(getattr(L, f"dh_plugin_{nm}"), C.c_void_p).value
                         for nm in ("clear_all", "thin3", "swap_out", "add_out")}
+        # a plugin that decodes ids through decode_fn (ban_relation), its stub
+        # tokenizer (id -> word, DH_VOCAB ids) and the vocabulary table itself
+        self.relation_plugin = C.cast(L.dh_plugin_relation, C.c_void_p).value
+        self.decode_stub = C.cast(L.dh_decode_stub, C.c_void_p).value
+        L.dh_vocab_table.restype = C.c_void_p
+        self.vocab_table = L.dh_vocab_table()
+        self.vocab_size = 4096
+        L.dh_set_filter_plugin_decode.argtypes = [C.c_void_p, C.c_void_p]
 
     def sample(self, row, T, k, pen, hist, filtered=False):
         """row: float32 array, modified in place like the reference."""
@@ -47,12 +55,18 @@ class DropIn:
         return self.L.dh_sample_token_top_p(_ptr(row, _fp), len(row), C.c_float(T), k, C.c_float(p))
 
     def set_filter_ops(self, ban_last=0, ban_repeat=0, ban_ids=None):
-        ids = None if not ban_ids else np.ascontiguousarray(ban_ids, np.int32)
+        ids = None if ban_ids is None or len(ban_ids) == 0 else np.ascontiguousarray(ban_ids, np.int32)
         self.L.dh_set_filter_ops(ban_last, ban_repeat, _ptr(ids, _ip), 0 if ids is None else len(ids))
 
-    def set_filter_plugin(self, fn):
-        """fn: address of a lal_filter_topk function, or None."""
-        self.L.dh_set_filter_plugin(fn)
+    def set_filter_plugin(self, fn, decode=None):
+        """fn: address of a lal_filter_topk function, or None; decode: the
+        lal_token_decode_fn handed to it (None: NULL)."""
+        self.L.dh_set_filter_plugin_decode(fn, decode)
+
+    def decode(self, tok):
+        buf = C.create_string_buffer(128)
+        n = C.CFUNCTYPE(C.c_int, C.c_int, C.c_char_p, C.c_int)(self.decode_stub)(tok, buf, 127)
+        return buf.value[:n].decode()
 
     def srand(self, seed):
         self.L.dh_srand(seed)

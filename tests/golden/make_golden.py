@@ -117,6 +117,23 @@ def sampler_cases():
         add(variant="filtered", kind=kind, seed=2100 + j, V=V, T=T, k=[40, 128, 512][j % 3],
             pen=pen, n_hist=nh, hist_seed=50 + j, u_seed=4100 + j, dup=True,
             filter="antirepeat4" if j % 2 else None)
+    # rows holding nan / +inf (appended: the ids above stay as they were)
+    nan_kinds = ["nan_first", "nan_early", "nan_late", "nan_sparse", "nan_all", "inf_mix", "nan_inf"]
+    for variant in ("basic", "filtered"):
+        for i, kind in enumerate(nan_kinds):
+            for j, V in enumerate([1, 7, 64, 1000, 4096]):
+                k = [1, 5, 40, 64, 3][(i + j) % 5]
+                if variant == "filtered":
+                    k = [1, 5, 40, 200, 512][(i + j) % 5]
+                T = [0.7, 0.0, 1.0, 0.8, 1.3][(i + 2 * j) % 5]  # T = 0: greedy
+                nh = [0, 10, 64][(i + j) % 3]
+                add(variant=variant, kind=kind, seed=3000 + 100 * i + j, V=V, T=T, k=k,
+                    pen=[1.1, 1.0, 1.2][(i * 2 + j) % 3], n_hist=min(nh, 4 * V),
+                    hist_seed=60 + 7 * i + j, invalid=(j % 2 == 0), u_seed=5000 + 31 * i + j,
+                    hot=1 if kind == "nan_early" and V > 2 else None)  # penalise nans at ids 1, 2
+        for j, kind in enumerate(["nan_sparse", "nan_early", "inf_mix"]):
+            add(variant=variant, kind=kind, seed=3900 + j, V=152064, T=0.7, k=[40, 50, 64][j],
+                pen=1.1, n_hist=64, hist_seed=90 + j, u_seed=5900 + j)
     return cases
 
 

@@ -11,7 +11,9 @@ REF_SO = os.path.join(ROOT, "oracle", "_ref", "liblal_ref.so")
 
 VARIANT_BASIC = 0
 VARIANT_FILTERED = 1
-F_DRAW_GPT2 = 0x2
+F_DRAW_GPT2 = 0x2       # draw over every id: r == 0 -> 0 (gpt2_server.c, qwen_server.c)
+F_FALLBACK_ZERO = 0x4   # mini_server.c: 0 when no sum reaches r
+F_GREEDY_FILTER = 0x8   # mini_server.c: the argmax through the filter as a one-element mask
 
 _fp = C.POINTER(C.c_float)
 _ip = C.POINTER(C.c_int)
@@ -21,7 +23,8 @@ class Params(C.Structure):
     _fields_ = [("temperature", C.c_float), ("top_k", C.c_int), ("top_p", C.c_float),
                 ("rep_penalty", C.c_float), ("variant", C.c_int), ("flags", C.c_uint),
                 ("ban_last", C.c_int), ("ban_repeat", C.c_int), ("n_ban_ids", C.c_int),
-                ("ban_ids", _ip), ("mask_recent", C.c_int)]
+                ("ban_ids", _ip), ("mask_recent", C.c_int), ("has_last", C.c_int),
+                ("last_token", C.c_int), ("last_tokens", _ip)]
 
 
 class Info(C.Structure):
@@ -37,14 +40,25 @@ def _ptr(a, t):
 
 
 def make_params(temperature=0.8, top_k=40, top_p=0.0, rep_penalty=1.1, variant=VARIANT_BASIC,
-                flags=0, ban_last=0, ban_repeat=0, ban_ids=None, mask_recent=0):
+                flags=0, ban_last=0, ban_repeat=0, ban_ids=None, mask_recent=0, last_token=None,
+                last_tokens=None):
+    """last_token: the filter's last token for sample_row; last_tokens: per row
+    for sample_batch (both: in place of hist[n-1], as mini_server.c passes it)."""
     p = Params(temperature, top_k, top_p, rep_penalty, variant, flags, ban_last, ban_repeat,
-               0, None, mask_recent)
-    keep = None
+               0, None, mask_recent, 0, 0, None)
+    keep = []
     if ban_ids is not None and len(ban_ids):
-        keep = np.ascontiguousarray(ban_ids, dtype=np.int32)
-        p.n_ban_ids = len(keep)
-        p.ban_ids = keep.ctypes.data_as(_ip)
+        ids = np.ascontiguousarray(ban_ids, dtype=np.int32)
+        keep.append(ids)
+        p.n_ban_ids = len(ids)
+        p.ban_ids = ids.ctypes.data_as(_ip)
+    if last_token is not None:
+        p.has_last = 1
+        p.last_token = int(last_token)
+    if last_tokens is not None:
+        lt = np.ascontiguousarray(last_tokens, dtype=np.int32)
+        keep.append(lt)
+        p.last_tokens = lt.ctypes.data_as(_ip)
     p._keepalive = keep
     return p
 
@@ -85,7 +99,7 @@ class Oracle:
                           "norepeat6": self.filter_norepeat6}
 
     def sample_row(self, row, params, hist=None, allow=None, bias=None, u=0.5, filt=None,
-                   cand_cap=0):
+                   cand_cap=0, decode=None):
         """Returns (token, info, cand_ids, cand_probs, cand_kept); `row` is mutated."""
         assert row.dtype == np.float32 and row.flags.c_contiguous
         V = row.shape[0]
@@ -98,7 +112,7 @@ class Oracle:
             kept = np.zeros(cand_cap, np.uint8)
         tok = self.L.lal_oracle_sample_row(
             _ptr(row, _fp), V, C.byref(params), _ptr(h, _ip), 0 if h is None else len(h),
-            _ptr(allow, C.POINTER(C.c_uint32)), _ptr(bias, _fp), C.c_float(u), filt, None,
+            _ptr(allow, C.POINTER(C.c_uint32)), _ptr(bias, _fp), C.c_float(u), filt, decode,
             C.byref(info), cand_cap, _ptr(ids, _ip), _ptr(probs, _fp),
             _ptr(kept, C.POINTER(C.c_ubyte)))
         return tok, info, ids, probs, kept
@@ -186,6 +200,7 @@ class Reference:
             f.restype = C.c_int
             f.argtypes = [_fp, C.c_int, C.c_float, C.c_int, C.c_float, _ip, C.c_int]
         L.lal_ref_set_filter.argtypes = [C.c_void_p]
+        L.lal_ref_qwen7b_set_vocab.argtypes = [C.c_void_p, C.c_int]
         L.lal_ref_vocab_capacity.restype = C.c_int
         L.lal_ref_gpt2_vocab.restype = C.c_int
         L.lal_ref_gpt2_embd.restype = C.c_int
@@ -193,6 +208,13 @@ class Reference:
         L.lal_ref_gpt2_quantize_row.restype = C.c_float
         L.lal_ref_gpt2_quantize_row.argtypes = [_fp, C.POINTER(C.c_int8), C.c_int]
         L.lal_ref_recent_push.argtypes = [_ip, _ip, C.c_int]
+        L.lal_ref_qwen_server_sample.restype = C.c_int
+        L.lal_ref_qwen_server_sample.argtypes = [_fp, C.c_float, C.c_int, C.c_float, _ip, C.c_int,
+                                                 C.c_void_p]
+        L.lal_ref_qwen_server_vocab.restype = C.c_int
+        L.lal_ref_mini_server_sample.restype = C.c_int
+        L.lal_ref_mini_server_sample.argtypes = [_fp, C.c_int, C.c_float, C.c_int, C.c_float, _ip,
+                                                 C.c_int, C.c_int, C.c_void_p]
         for sfx in ("avx2", "scalar"):
             f = getattr(L, f"lal_ref_quantize_x_int8_{sfx}")
             f.restype = C.c_float
@@ -215,6 +237,22 @@ class Reference:
         q = np.zeros(len(x), np.int8)
         s = self.L.lal_ref_gpt2_quantize_row(_ptr(x, _fp), _ptr(q, C.POINTER(C.c_int8)), len(x))
         return np.float32(s), q
+
+    def qwen_server_sample(self, row, T, k, pen, hist, seed, filt=None):
+        """tools/server/qwen_server.c:418-527 over a row of its VOCAB_SIZE
+        (151936) ids; the row is penalised in place."""
+        h = np.zeros(1, np.int32) if hist is None else np.ascontiguousarray(hist, np.int32)
+        assert len(row) == self.L.lal_ref_qwen_server_vocab()
+        self.L.lal_ref_srand(seed)
+        return self.L.lal_ref_qwen_server_sample(_ptr(row, _fp), C.c_float(T), k, C.c_float(pen),
+                                                 _ptr(h, _ip), 0 if hist is None else len(h), filt)
+
+    def mini_server_sample(self, row, T, k, pen, hist, last_tok, seed, filt=None):
+        """tools/mini_server.c:267-363 (the row is copied, not modified)."""
+        h = np.zeros(1, np.int32) if hist is None else np.ascontiguousarray(hist, np.int32)
+        self.L.lal_ref_srand(seed)
+        return self.L.lal_ref_mini_server_sample(_ptr(row, _fp), len(row), C.c_float(T), k, C.c_float(pen),
+                                                 _ptr(h, _ip), 0 if hist is None else len(h), last_tok, filt)
 
     def sample(self, row, V, T, k, pen, hist, seed, filtered=False, filt=None):
         h = None if hist is None else np.ascontiguousarray(hist, np.int32)

@@ -159,4 +159,44 @@ def make_row(kind, seed, V):
         return x.astype(np.float32)
     if kind == "huge":  # magnitudes near the fp32 range
         return (normal(seed, 0, V) * np.float32(1e37)).astype(np.float32)
+    # Rows a diverging model produces.  A nan compares false with everything,
+    # so where it sits decides what the reference's heap and argmax do.
+    qnan, neg_qnan = _bits_f32(0x7FC00000), _bits_f32(0xFFC00000)
+    if kind == "nan_first":  # id 0 is nan: the greedy scan keeps id 0
+        x = normal(seed, 0, V) * np.float32(2.5)
+        x[0] = qnan
+        return x.astype(np.float32)
+    if kind == "nan_early":  # nans among the first ids: they enter the heap while it fills
+        x = normal(seed, 0, V) * np.float32(2.5)
+        x[1:12:3] = qnan
+        x[2:12:5] = neg_qnan
+        return x.astype(np.float32)
+    if kind == "nan_late":  # one nan after the heap has filled, next to the largest values
+        x = normal(seed, 0, V) * np.float32(2.5)
+        if V > 1:
+            x[V // 2] = qnan
+            x[min(V - 1, V // 2 + 1)] = np.float32(9.0)
+        return x.astype(np.float32)
+    if kind == "nan_sparse":  # ~2 % nans of both signs, spread over the row
+        x = normal(seed, 0, V) * np.float32(2.5)
+        u = uniform(seed, 91, V)
+        x[u < np.float32(0.01)] = qnan
+        x[(u >= np.float32(0.01)) & (u < np.float32(0.02))] = neg_qnan
+        return x.astype(np.float32)
+    if kind == "nan_all":
+        return np.full(V, qnan, np.float32)
+    if kind == "inf_mix":  # a few +inf (ties at the top) and -inf
+        x = normal(seed, 0, V) * np.float32(2.5)
+        u = uniform(seed, 92, V)
+        x[u < np.float32(0.002)] = np.inf
+        x[(u >= np.float32(0.002)) & (u < np.float32(0.05))] = -np.inf
+        return x.astype(np.float32)
+    if kind == "nan_inf":  # nan, +inf and -inf together
+        x = make_row("inf_mix", seed, V)
+        x[uniform(seed, 93, V) < np.float32(0.01)] = qnan
+        return x.astype(np.float32)
     raise ValueError(kind)
+
+
+def _bits_f32(bits):
+    return np.array([bits], np.uint32).view(np.float32)[0]

@@ -75,7 +75,10 @@ def test_malformed_files_are_errors(lib, tmp_path):
     good = G.image([G.record("w", np.ones((3, 4), np.float32), G.F32),
                     G.record("s", np.ones((2, 8), np.int8), G.Q8, scale=np.ones(2, np.float32))])
     cases = {"magic": b"GPQ9" + good[4:], "count": good[:4] + (5).to_bytes(4, "little") + good[8:],
-             "empty": b"", "short": good[:6]}
+             "empty": b"", "short": good[:6],
+             # a tensor count the file cannot hold (once an allocation abort)
+             "hugecount": b"GPQ8" + (0x7fffffff).to_bytes(4, "little"),
+             "hugecount_tail": b"GPQ8" + (0x7fffffff).to_bytes(4, "little") + good[8:]}
     for cut in range(9, len(good), 7):  # every truncation point inside the directory
         cases[f"cut{cut}"] = good[:cut]
     neg = bytearray(good)

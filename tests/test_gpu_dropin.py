@@ -107,3 +107,43 @@ def test_generation_loop_qwen7b_vocab(dh, orc):
         ring_ora.append(int(o["token"][0]))
     assert ring_dev == ring_ora
     log(f"generation loop: {ring_dev[:8]} ...")
+
+
+def test_ban_ids_survive_context_growth(dh, orc):
+    """ban_token ids set before the first sample (on a vocab-1 context) are
+    kept when the first filtered call at V = 152064 re-creates the device
+    buffers, and again when a larger vocabulary arrives later."""
+    for V, seed in ((4099, 1), (152064, 2)):
+        dh.L.dh_release()  # a fresh context, as at server start-up
+        row = synth.make_row("outliers", 7300 + seed, V)
+        hist = synth.history(7400 + seed, 1, 16, V)[0]
+        # ban the top tokens of the row, so that the bans decide the draw
+        top = np.argsort(-row, kind="stable")[:6].astype(np.int32)
+        dh.set_filter_ops(ban_ids=top)
+        for step, vocab in enumerate((V // 2, V)):  # the second call grows the context
+            r = row[:vocab].copy()
+            h = hist[hist < vocab]
+            dh.srand(500 + step)
+            tok = dh.sample(r, 0.7, 40, 1.1, h, filtered=True)
+            u = orc.uniforms(500 + step, 1)
+            o = oracle_run(orc, row[None, :vocab], T=0.7, k=40, pen=1.1, variant=1, hist=h[None, :], u=u,
+                           ban_ids=top)
+            log(f"ban ids V={vocab}: drop-in {tok} oracle {int(o['token'][0])}")
+            assert tok == int(o["token"][0])
+            assert tok not in set(top.tolist()) or int(o["n_kept"][0]) == int(o["n_cand"][0])
+    dh.set_filter_ops()
+
+
+@pytest.mark.parametrize("filtered,V,k", [(True, 300, 1000), (True, 512, 4096), (False, 50, 1000)])
+def test_top_k_above_vocab(dh, orc, filtered, V, k):
+    """top_k above the vocabulary is clamped to it and sampled, as
+    tools/server/qwen7b_server.c:236 does (no error for k > 512 when V <= 512)."""
+    row = synth.make_row("gauss", 7500 + V, V)
+    hist = synth.history(7600 + V, 1, 8, V)[0]
+    x = row.copy()
+    dh.srand(31)
+    tok = dh.sample(x, 0.9, k, 1.1, hist, filtered=filtered)
+    o = oracle_run(orc, row[None, :], T=0.9, k=k, pen=1.1, variant=1 if filtered else 0, hist=hist[None, :],
+                   u=orc.uniforms(31, 1))
+    assert tok == int(o["token"][0])
+    assert np.array_equal(x.view(np.uint32), o["logits_after"][0].view(np.uint32))

@@ -222,3 +222,63 @@ def test_plugins_through_dropin(dh, orc):
                     assert nxt == stream_after(dh, seed, 1 if info.sum > 0 else 0)
                     cases += 1
     log(f"{cases} plugin cases")
+
+
+def test_relation_plugin_with_decode_fn(dh, orc):
+    """A plugin that decodes ids through decode_fn (ban_last, ban_repeat(6)
+    and the ban_relation rules of demos/qwen_filter.lal, following
+    compiler/lal.py:2243-2317), loaded with lal_sampling_set_filter_plugin(fn,
+    decode): the drop-in hands the plugin the caller's decode function and the
+    recent ids, as tools/server/qwen7b_server.c:257-264 does.  Checked against
+    the oracle with the same plugin and decoder, and against the reference's
+    lal_sample_token_filtered with the plugin loaded and the stub vocabulary
+    installed as its tokenizer (so its own decode_fn decodes the same words)."""
+    ref = Reference() if os.path.exists(REF_SO) else None
+    V = dh.vocab_size
+    if ref is not None:
+        ref.L.lal_ref_qwen7b_set_vocab(dh.vocab_table, V)
+    assert dh.decode(6) == " Paris" and dh.decode(20) == " xcapital"
+    paris, tokyo = [6, 10, 11, 9, 12], [7, 15, 16, 17]
+    histories = {
+        "france": [40, 41, 0, 1, 2, 3],           # "... the capital of France": keep " Paris", " Paris."
+        "japan": [42, 0, 1, 2, 4],               # "... the capital of Japan": keep " Tokyo"
+        "no_trigger": [0, 1, 2, 3, 14],          # ends with " city"
+        "no_boundary": [43, 20, 2, 3],           # " xcapital of France": 'x' before the trigger
+        "nothing_allowed": [0, 1, 2, 3],         # France, but no Paris in the pool: restored
+    }
+    cases = 0
+    for name, hist in histories.items():
+        for k in (1, 5, 40, 512):
+            row = synth.make_row("gauss", 8800 + k, V)
+            hot = [i for i in paris + tokyo] if name != "nothing_allowed" else [7, 17, 44, 45]
+            for j, t in enumerate(hot):
+                row[t] = np.float32(9.0 - 0.25 * j)
+            h = np.array(hist, np.int32)
+            seed = 8900 + k + len(name)
+            u = float(orc.uniforms(seed, 1)[0])
+            r_o = row.copy()
+            tok_o, info, _, _, _ = orc.sample_row(
+                r_o, oparams(temperature=0.8, top_k=k, rep_penalty=1.1, variant=abi.VARIANT_FILTERED),
+                hist=h, u=u, filt=dh.relation_plugin, decode=dh.decode_stub)
+            if ref is not None:
+                r_r = row.copy()
+                tok_r = ref.sample(r_r, V, 0.8, k, 1.1, h, seed, filtered=True, filt=dh.relation_plugin)
+                assert tok_r == tok_o, f"oracle vs reference: {name} k={k}: {tok_o} vs {tok_r}"
+            dh.set_filter_plugin(dh.relation_plugin, dh.decode_stub)
+            x = row.copy()
+            dh.srand(seed)
+            tok = dh.sample(x, 0.8, k, 1.1, h, filtered=True)
+            nxt = dh.rand()
+            dh.set_filter_plugin(None)
+            log(f"relation plugin {name} k={k}: drop-in {tok} ({dh.decode(tok)!r}) oracle {tok_o}")
+            assert tok == tok_o, f"{name} k={k}"
+            assert np.array_equal(x.view(np.uint32), r_o.view(np.uint32))
+            assert nxt == stream_after(dh, seed, 1 if info.sum > 0 else 0)
+            if name == "france" and k >= 5:
+                assert dh.decode(tok) in (" Paris", " Paris."), dh.decode(tok)
+            if name == "japan" and k >= 40:  # the top 5 hold no " Tokyo": emptied, then restored
+                assert dh.decode(tok) == " Tokyo"
+            cases += 1
+    if ref is not None:
+        ref.L.lal_ref_qwen7b_set_vocab(None, 0)
+    log(f"{cases} relation-plugin cases")

@@ -1,0 +1,117 @@
+"""The Q8 LM head + sampling step (tools/server/qwen7b_server.c:829-848) at the
+Qwen2.5-7B shape, end to end on the GPU, against the CPU oracle on the same
+bytes.
+
+GPU: lal_gpu_quantize_x (AVX2-build rounding) -> lal_gpu_lm_head_q8_packed
+(W [152064, 3584] int8 in the load-time packed layout) -> lal_gpu_sample
+(penalty 1.1 over 64 ids, T 0.7, top-k 40, one uniform per row), all on the
+device.  Oracle: lal_oracle_quantize_x -> lal_oracle_lm_head over all 152064
+vocabulary rows -> lal_oracle_sample_batch.  Bar: every logit, token id,
+threshold, pool size, pool membership and softmax sum bit-exact;
+probabilities within 1e-5 relative."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+import synth
+from gpu_helpers import assert_same, log, oracle_run
+from oracle_lib import Oracle
+
+pytestmark = pytest.mark.gpu
+
+V, N = 152064, 3584
+
+
+@pytest.fixture(scope="module")
+def dev():
+    from lal_amd import abi
+    d = abi.Device(0, max_batch=64, max_vocab=V)
+    yield d
+    d.close()
+
+
+@pytest.fixture(scope="module")
+def orc():
+    return Oracle()
+
+
+@pytest.fixture(scope="module")
+def head(dev):
+    """W int8 uniform in [-127, 127], sw ~ U(0.001, 0.02), generated on the GPU;
+    the packed copy the matrix-core head reads; host copies for the oracle."""
+    from lal_amd import abi
+    dW = dev.alloc(V * N)
+    abi.check(dev.lib.lal_gpu_synth_int8(dW.ptr, V * N, 4242, -127, 127, dev.stream), "synth W")
+    dsw = dev.alloc(4 * V)
+    abi.check(dev.lib.lal_gpu_synth_uniform(dsw.ptr, V, 4243, C.c_float(0.001), C.c_float(0.02),
+                                            dev.stream), "synth sw")
+    dpk = dev.alloc(dev.lib.lal_gpu_q8_packed_bytes(V, N))
+    abi.check(dev.lib.lal_gpu_pack_q8(dev.ctx, dW.ptr, V, N, dpk.ptr, dev.stream), "pack")
+    dev.sync()
+    W = dW.download((V, N), np.int8)
+    sw = dsw.download(V, np.float32)
+    dW.close()
+    yield dict(dpk=dpk, dsw=dsw, W=W, sw=sw)
+    dpk.close()
+    dsw.close()
+
+
+def gpu_step(dev, head, x, hist, u, T=0.7, k=40, pen=1.1, cand_ld=64):
+    """quantize -> packed LM head -> sampler on the device; returns the logits
+    and every sampler output."""
+    from lal_amd import abi
+    B = x.shape[0]
+    bufs = dict(x=dev.put(x), xq=dev.alloc(B * N), sx=dev.alloc(4 * B), logits=dev.alloc(4 * B * V),
+                hist=dev.put(hist), u=dev.put(u))
+    outs = {"token": (B, np.int32), "threshold": (B, np.float32), "n_cand": (B, np.int32),
+            "n_kept": (B, np.int32), "sum": (B, np.float32)}
+    for name, (n, dt) in outs.items():
+        bufs[name] = dev.alloc(n * np.dtype(dt).itemsize)
+    for name, size in (("cids", 4), ("cprobs", 4), ("ckept", 1), ("cvals", 4)):
+        bufs[name] = dev.alloc(size * B * cand_ld)
+    abi.check(dev.lib.lal_gpu_quantize_x(dev.ctx, bufs["x"].ptr, B, N, 0, bufs["xq"].ptr, bufs["sx"].ptr,
+                                         dev.stream), "quantize_x")
+    abi.check(dev.lib.lal_gpu_lm_head_q8_packed(dev.ctx, bufs["xq"].ptr, bufs["sx"].ptr, B, N,
+                                                head["dpk"].ptr, head["dsw"].ptr, V, bufs["logits"].ptr, V,
+                                                dev.stream), "lm_head_q8_packed")
+    io = abi.SampleIO(logits=bufs["logits"].ptr, ld=V, history=bufs["hist"].ptr,
+                      history_ld=hist.shape[1], uniforms=bufs["u"].ptr, out_token=bufs["token"].ptr)
+    io.out_threshold = bufs["threshold"].ptr
+    io.out_n_cand = bufs["n_cand"].ptr
+    io.out_n_kept = bufs["n_kept"].ptr
+    io.out_sum = bufs["sum"].ptr
+    io.cand_ld = cand_ld
+    io.cand_ids = bufs["cids"].ptr
+    io.cand_probs = bufs["cprobs"].ptr
+    io.cand_kept = bufs["ckept"].ptr
+    io.cand_vals = bufs["cvals"].ptr
+    dev.sample(B, V, abi.make_params(temperature=T, top_k=k, rep_penalty=pen), io)
+    dev.sync()
+    res = {name: bufs[name].download(n, dt) for name, (n, dt) in outs.items()}
+    res["cand_ids"] = bufs["cids"].download((B, cand_ld), np.int32)
+    res["cand_probs"] = bufs["cprobs"].download((B, cand_ld), np.float32)
+    res["cand_kept"] = bufs["ckept"].download((B, cand_ld), np.uint8)
+    logits = bufs["logits"].download((B, V), np.float32)
+    for b in bufs.values():
+        b.close()
+    return logits, res
+
+
+@pytest.mark.parametrize("B", [1, 16, 64])
+def test_q8_head_then_sampler(dev, orc, head, B):
+    x = (synth.normal(6100 + B, 0, B * N).reshape(B, N)).astype(np.float32)
+    hist = synth.history(6200 + B, B, 64, V)
+    u = orc.uniforms(6300 + B, B)
+    log(f"config-5 step B={B}: GPU quantize -> packed LM head -> sampler")
+    logits, got = gpu_step(dev, head, x, hist, u)
+    log(f"config-5 step B={B}: oracle quantize -> LM head over {V} rows -> sampler")
+    want_logits = np.empty((B, V), np.float32)
+    for b in range(B):
+        sx, xq = orc.quantize_x(x[b].copy(), 0)
+        want_logits[b] = orc.lm_head(xq, sx, head["W"], head["sw"])
+    bad = np.nonzero(logits.view(np.uint32) != want_logits.view(np.uint32))
+    assert len(bad[0]) == 0, f"logits differ at {list(zip(bad[0][:5], bad[1][:5]))}"
+    want = oracle_run(orc, want_logits, T=0.7, k=40, pen=1.1, hist=hist, u=u, cand_ld=64)
+    assert_same(got, want, cand_ld=64)
+    log(f"config-5 step B={B}: {B} tokens, pools and logits bit-exact")

@@ -154,7 +154,8 @@ def test_constrained_decoding(dev, run, orc):
 # ---------------------------------------------------------------------------
 @pytest.mark.parametrize("variant", [0, 1])
 @pytest.mark.parametrize("kind", ["gauss", "ties", "neginf", "ascending", "const", "allneginf",
-                                  "signed_zero", "huge", "zipf"])
+                                  "signed_zero", "huge", "zipf", "nan_first", "nan_early",
+                                  "nan_late", "nan_sparse", "nan_all", "inf_mix", "nan_inf"])
 def test_row_kinds(run, orc, variant, kind):
     B, V = 6, 20011
     x = np.stack([synth.make_row(kind, 31 * b + 1, V) for b in range(B)])
@@ -308,3 +309,66 @@ def test_pool_above_buffers_with_top_p(run, orc, slices, nsl):
         kw = dict(T=0.8, k=k, top_p=top_p, pen=1.1, hist=hist, u=u, cand_ld=64, ban_last=1)
         log(f"rescan top-p slices {nsl} k {k} p {top_p}")
         assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=64)
+
+
+def test_top_k_clamped_before_the_limit(dev, run, orc):
+    """top_k is clamped to the vocabulary before the LAL_GPU_MAX_K check: k =
+    1000 over V = 300 samples (the pool is the whole row); min(k, V) above 512
+    is an error, not a silent result."""
+    from lal_amd import abi
+    B, V = 4, 300
+    x = np.stack([synth.make_row("gauss", 90 + b, V) for b in range(B)])
+    hist = synth.history(91, B, 8, V)
+    u = orc.uniforms(92, B)
+    for variant in (0, 1):
+        kw = dict(T=0.9, k=1000, pen=1.1, variant=variant, hist=hist, u=u, cand_ld=V)
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=V)
+    big = np.stack([synth.make_row("gauss", 93, 2000)])
+    with pytest.raises(abi.GpuError, match="rc=-2"):
+        run(big, T=0.9, k=600, pen=1.1, u=orc.uniforms(94, 1))
+
+
+# ---------------------------------------------------------------------------
+# the other reference samplers as parameter sets
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("kind", ["gauss", "zipf", "allneginf", "inf_mix", "nan_sparse", "ties"])
+def test_qwen_server_parameter_set(run, orc, kind):
+    """tools/server/qwen_server.c:418-527: VARIANT_BASIC with the draw over
+    every id (r == 0 gives id 0) and the anti-repeat bans on the pool, over
+    its 151936-id vocabulary."""
+    from lal_amd import abi
+    B, V = 6, 151936
+    x = np.stack([synth.make_row(kind, 9500 + b, V) for b in range(B)])
+    hist = synth.history(9600, B, 64, V)
+    u = np.array([0.0, 1.0, 0.5, 0.123, 0.999, 1e-7], np.float32)
+    for T, k, bans in ((0.8, 40, {}), (0.7, 5, dict(ban_last=1, ban_repeat=4)), (0.0, 40, {})):
+        kw = dict(T=T, k=k, pen=1.1, variant=abi.VARIANT_BASIC, flags=abi.F_DRAW_ALL_IDS, hist=hist, u=u,
+                  cand_ld=64, **bans)
+        log(f"qwen_server set {kind} T={T} k={k} {bans}")
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=64)
+
+
+@pytest.mark.parametrize("V", [65, 4099, 20011])
+def test_mini_server_parameter_set(run, orc, V):
+    """tools/mini_server.c:267-363: VARIANT_FILTERED, 0 as the draw's fallback,
+    the argmax through the bans as a one-element mask, the caller's last token
+    for ban_last, no write-back (the row is penalised in a copy)."""
+    from lal_amd import abi
+    kinds = ["gauss", "inf_mix", "nan_early", "zipf", "allneginf", "descending", "ties", "nan_inf"]
+    B = len(kinds)
+    x = np.stack([synth.make_row(kinds[b], 9700 + b, V) for b in range(B)])
+    hist = synth.history(9800 + V, B, 24, V)
+    hist[::3, -1] = 0  # rows whose last history id is 0
+    last = synth.ints(9900 + V, 0, B, -1, V)
+    last[::2] = 0
+    u = synth.uniform(9901, 0, B)
+    u[1] = 0.0
+    flags = abi.F_FALLBACK_ZERO | abi.F_GREEDY_FILTER
+    for T, k, bans in ((0.9, 8, dict(ban_last=1)), (0.0, 8, dict(ban_last=1)),
+                       (0.0, 8, dict(ban_repeat=4)), (0.0, 8, dict(ban_ids=[0, 5])),
+                       (0.7, 300, dict(ban_last=1, ban_repeat=6)), (1.1, 1, {}), (0.0, 40, {})):
+        kw = dict(T=T, k=k, pen=1.15, variant=abi.VARIANT_FILTERED, flags=flags, hist=hist, u=u,
+                  cand_ld=320, last_tokens=last, **bans)
+        log(f"mini_server set V={V} T={T} k={k} {bans}")
+        g = run(x, **kw)
+        assert_same(g, oracle_run(orc, x, **kw), cand_ld=320)

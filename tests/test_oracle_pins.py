@@ -284,3 +284,94 @@ def test_gpt2_rerank_against_reference(ref, seed, ties, strong):
         assert 0 < r < len(eq), "ties straddle the boundary"
         kept = set(ids.tolist())
         assert kept != above | set(eq[:r]) and kept != above | set(eq[-r:])
+
+
+# ---------------------------------------------------------------------------
+# The other reference samplers as oracle flags (pinned against the servers'
+# own sample_next_token, compiled in oracle/_ref)
+# ---------------------------------------------------------------------------
+from oracle_lib import F_DRAW_GPT2, F_FALLBACK_ZERO, F_GREEDY_FILTER  # noqa: E402
+
+QWEN_SERVER_KINDS = ["gauss", "zipf", "ties", "outliers", "neginf", "allneginf", "inf_mix",
+                     "nan_sparse", "nan_first", "const"]
+
+
+@pytest.mark.parametrize("i", range(len(QWEN_SERVER_KINDS)))
+def test_qwen_server_sampler_against_reference(ref, i):
+    """tools/server/qwen_server.c:418-527 = variant BASIC (greedy before the
+    penalty, heap of 64) with the draw over every id (F_DRAW_GPT2: r == 0 gives
+    id 0, no sum <= 0 branch), plugins on the keep mask with the restore."""
+    V = ref.L.lal_ref_qwen_server_vocab()
+    kind = QWEN_SERVER_KINDS[i]
+    row = synth.make_row(kind, 7700 + i, V)
+    for j, (T, k, pen, nh, filt) in enumerate([(0.8, 40, 1.1, 64, None), (0.0, 40, 1.2, 16, None),
+                                               (1.3, 64, 1.0, 0, None), (0.7, 5, 1.3, 256, "antirepeat4"),
+                                               (0.9, 1, 1.1, 8, "norepeat6"), (0.8, 0, 1.1, 32, None)]):
+        hist = synth.history(7800 + 10 * i + j, 1, nh, V, with_invalid=(j % 2 == 1))[0] if nh else None
+        seed = 7900 + 10 * i + j
+        fptr = ORC.filter_fn[filt] if filt else None
+        want = row.copy()
+        tok_ref = ref.qwen_server_sample(want, T, k, pen, hist, seed, filt=fptr)
+        got = row.copy()
+        u = ORC.uniforms(seed, 1)[0]
+        p = make_params(temperature=T, top_k=k, rep_penalty=pen, variant=VARIANT_BASIC, flags=F_DRAW_GPT2)
+        tok, *_ = ORC.sample_row(got, p, hist=hist, u=u, filt=fptr)
+        assert tok == tok_ref, f"{kind} case {j}: oracle {tok} reference {tok_ref}"
+        assert synth.digest(got) == synth.digest(want), f"{kind} case {j}: in-place penalty"
+
+
+MINI_KINDS = ["gauss", "zipf", "ties", "outliers", "neginf", "allneginf", "inf_mix", "nan_early",
+              "nan_all", "const", "descending"]
+
+
+@pytest.mark.parametrize("i", range(len(MINI_KINDS)))
+def test_mini_server_sampler_against_reference(ref, i):
+    """tools/mini_server.c:267-363 = variant FILTERED (penalty first, k in
+    [1, V], heap of 512, sum <= 0 -> argmax of the kept set) on a copy of the
+    row, 0 as the draw's fallback (F_FALLBACK_ZERO), the argmax through the
+    filter as a one-element keep mask (F_GREEDY_FILTER) and the caller's last
+    token as the filter's `last`."""
+    kind = MINI_KINDS[i]
+    for j, V in enumerate([7, 65, 1000, 4099]):
+        row = synth.make_row(kind, 8100 + 10 * i + j, V)
+        for c, (T, k, pen, nh, filt) in enumerate([(0.9, 8, 1.15, 24, None), (0.0, 8, 1.2, 12, None),
+                                                   (0.7, 300, 1.1, 40, "antirepeat4"),
+                                                   (1.1, 3, 1.0, 6, "norepeat6"), (0.8, 1, 1.3, 64, None),
+                                                   (0.0, 40, 1.1, 5, "antirepeat4")]):
+            hist = synth.history(8200 + 100 * i + 10 * j + c, 1, nh, V)[0]
+            last_tok = int(synth.ints(8300 + i, j * 10 + c, 1, -1, V)[0])
+            if T <= 0 and filt:
+                # the reference hands the plugin a one-element array (&km) with
+                # n_vocab = V: ids other than 0 would be read past it, so these
+                # cases keep every id the plugin looks at in {0} or out of range
+                hist = np.where(np.arange(nh) % 2 == 0, 0, V + 3).astype(np.int32)
+                last_tok = [0, -1][c % 2]
+            seed = 8400 + 100 * i + 10 * j + c
+            fptr = ORC.filter_fn[filt] if filt else None
+            base = row.copy()
+            tok_ref = ref.mini_server_sample(base, T, k, pen, hist, last_tok, seed, filt=fptr)
+            assert np.array_equal(base.view(np.uint32), row.view(np.uint32)), "mini_server penalises a copy"
+            got = row.copy()
+            u = ORC.uniforms(seed, 1)[0]
+            p = make_params(temperature=T, top_k=k, rep_penalty=pen, variant=VARIANT_FILTERED,
+                            flags=F_FALLBACK_ZERO | F_GREEDY_FILTER, last_token=last_tok)
+            tok, *_ = ORC.sample_row(got, p, hist=hist, u=u, filt=fptr)
+            assert tok == tok_ref, f"{kind} V={V} case {c}: oracle {tok} reference {tok_ref}"
+
+
+def test_mini_greedy_filter_clears_id_zero():
+    """F_GREEDY_FILTER: a ban of id 0 (here ban_last with last token 0) turns
+    the greedy token into 0; bans of other ids leave it.  Without the flag the
+    bans do not touch a greedy row."""
+    V = 500
+    row = synth.make_row("gauss", 8500, V)
+    best = int(np.argmax(row))
+    assert best != 0
+    for last, want in ((0, 0), (5, best), (best, best)):
+        p = make_params(temperature=0.0, top_k=8, rep_penalty=1.0, variant=VARIANT_FILTERED,
+                        flags=F_GREEDY_FILTER, ban_last=1, last_token=last)
+        tok, *_ = ORC.sample_row(row.copy(), p, u=0.5)
+        assert tok == want, (last, tok, want)
+        p.flags = 0
+        tok, *_ = ORC.sample_row(row.copy(), p, u=0.5)
+        assert tok == best
