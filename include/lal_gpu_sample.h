@@ -190,6 +190,24 @@ int  lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab,
                     const lal_gpu_sample_params *params,
                     const lal_gpu_sample_io *io, void *stream);
 
+/* lal_gpu_sample without a context and without allocating: no counterpart in
+ * the reference.  For callers that cannot allocate device memory on the
+ * sampling path (code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc).  Same arguments, checks and results as
+ * lal_gpu_sample, on the current device; it calls no hipMalloc or hipFree.
+ * The candidate lists that the workgroups of a sliced row exchange live in a
+ * static per-device scratch array of LAL_GPU_NOALLOC_MAX_ROWS rows (about
+ * 4.3 MB, held by each GPU the library runs on until the process ends), set up
+ * on the first call on each device.  Batches of up to that many rows are
+ * sliced as lal_gpu_sample slices them; larger batches run one workgroup per
+ * row and use no scratch (results never depend on slicing).  A forced slice
+ * count (LAL_GPU_SLICES) with a larger batch is LAL_GPU_E_RANGE.  Every call
+ * on one GPU shares that GPU's scratch: calls that overlap on one GPU (two
+ * streams, two threads) race; calls in one stream order are safe. */
+#define LAL_GPU_NOALLOC_MAX_ROWS 64
+int  lal_gpu_sample_noalloc(int batch, int vocab, const lal_gpu_sample_params *params,
+                            const lal_gpu_sample_io *io, void *stream);
+
 int  lal_gpu_sample_finish(lal_gpu_ctx *ctx, int batch, int vocab,
                            const lal_gpu_sample_params *params,
                            const lal_gpu_finish_io *io, void *stream);

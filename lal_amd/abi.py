@@ -24,6 +24,7 @@ ABI_VERSION = 3
 MAX_K = 512
 MAX_HISTORY = 512
 MAX_BAN_IDS = 64
+NOALLOC_MAX_ROWS = 64
 
 ERRORS = {0: "ok", -1: "invalid argument", -2: "size above a limit", -3: "HIP error",
           -4: "out of device memory", -5: "no such device"}
@@ -78,6 +79,7 @@ EXPORTS = [
     ("lal_gpu_destroy", None, [_vp]),
     ("lal_gpu_sample", _i, [_vp, _i, _i, C.POINTER(SampleParams), C.POINTER(SampleIO), _vp]),
     ("lal_gpu_sample_finish", _i, [_vp, _i, _i, C.POINTER(SampleParams), C.POINTER(FinishIO), _vp]),
+    ("lal_gpu_sample_noalloc", _i, [_i, _i, C.POINTER(SampleParams), C.POINTER(SampleIO), _vp]),
     ("lal_gpu_quantize_x", _i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
     ("lal_gpu_lm_head_q8", _i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
     ("lal_gpu_q8_packed_bytes", _sz, [_i, _i]),

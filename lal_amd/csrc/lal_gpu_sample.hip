@@ -30,6 +30,7 @@
 
 #include <algorithm>
 #include <climits>
+#include <mutex>
 #include <math.h>
 #include <stdint.h>
 #include <stdlib.h>
@@ -3816,12 +3817,26 @@ static int choose_slices(int batch, int vocab, int k_eff, int flat, int forced)
     return std::max(1, std::min(n, MAX_SLICES));
 }
 
-int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_params *p,
-                   const lal_gpu_sample_io *io, void *stream)
+}  // extern "C"
+
+// Where a launch's slice lists live (a context's buffers or the static
+// scratch of lal_gpu_sample_noalloc) and the device facts the launch needs.
+struct ListTarget {
+    int ncu;
+    int forced_slices;
+    int slice_rows;  // batches up to this many rows may be sliced; larger ones
+                     // run one workgroup per row and touch no list
+    float *lst_val;
+    int *lst_idx;
+    int4 *lst_meta;
+    unsigned *arrive;
+};
+
+static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gpu_sample_params *p,
+                         const lal_gpu_sample_io *io, void *stream)
 {
-    if (!ctx || !p || !io) return LAL_GPU_E_INVAL;
+    if (!p || !io) return LAL_GPU_E_INVAL;
     if (batch <= 0 || vocab <= 0) return LAL_GPU_E_INVAL;
-    if (batch > ctx->max_batch || vocab > ctx->max_vocab) return LAL_GPU_E_RANGE;
     if (!io->logits || !io->out_token || io->ld < vocab) return LAL_GPU_E_INVAL;
     const bool greedy = !(p->temperature > 0.0f) || p->top_k <= 0;
     // top_k is clamped to the vocabulary first, as the kernel and the
@@ -3903,17 +3918,17 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     const bool small = k_eff <= K_SMALL_MAX;
     const int flat = NWAVE * (small ? CAPW_SMALL : CAPW_LARGE);
     A.batch = batch;
-    A.nslice = choose_slices(batch, vocab, k_eff, flat, ctx->forced_slices);
-    A.ncu = ctx->ncu;
+    A.nslice = (batch <= t.slice_rows) ? choose_slices(batch, vocab, k_eff, flat, t.forced_slices) : 1;
+    A.ncu = t.ncu;
     A.lcap = flat / A.nslice;
     // a slice list must hold more than k values (see the finisher): always
     // true by choose_slices, checked so that the kernel's overflow branch
     // stays unreachable
     if (A.nslice > 1 && A.lcap <= k_eff) return LAL_GPU_E_RANGE;
-    A.lst_val = ctx->lst_val;
-    A.lst_idx = ctx->lst_idx;
-    A.lst_meta = ctx->lst_meta;
-    A.arrive = ctx->arrive;
+    A.lst_val = t.lst_val;
+    A.lst_idx = t.lst_idx;
+    A.lst_meta = t.lst_meta;
+    A.arrive = t.arrive;
     const dim3 grid((unsigned)(((batch + 7) / 8) * 8 * A.nslice)), block(WG);
 #define LAL_LAUNCH(HB, HA)                                                                   \
     do {                                                                                     \
@@ -3929,6 +3944,98 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
 #undef LAL_LAUNCH
     LAL_HIP(hipGetLastError());
     return LAL_GPU_OK;
+}
+
+// ---- the sampler without allocation ---------------------------------------
+// Candidate lists and arrival counters of up to LAL_GPU_NOALLOC_MAX_ROWS sliced
+// rows, in one file-scope device array: each GPU the library runs on holds its
+// own copy (about 4.3 MB) until the process ends.  Host code never uses the
+// array's name as an address: its device address comes from
+// hipGetSymbolAddress, once per device, with that device current.
+struct NoallocScratch {
+    float lst_val[LAL_GPU_NOALLOC_MAX_ROWS * FLAT_MAX];
+    int lst_idx[LAL_GPU_NOALLOC_MAX_ROWS * FLAT_MAX];
+    int4 lst_meta[LAL_GPU_NOALLOC_MAX_ROWS * MAX_SLICES];
+    unsigned arrive[LAL_GPU_NOALLOC_MAX_ROWS];
+};
+static __device__ __align__(256) NoallocScratch scratch;
+
+namespace {
+// the arrival counters start at zero (each row's finisher resets its own)
+__global__ void clear_u32_kernel(unsigned *p, int n)
+{
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0u;
+}
+
+constexpr int NOALLOC_MAX_DEVICES = 64;
+struct NoallocDevice {
+    std::once_flag once;
+    int rc = LAL_GPU_OK;
+    int ncu = 0;
+    int forced_slices = 0;
+    NoallocScratch *ptr = nullptr;  // this device's copy of `scratch`
+};
+NoallocDevice g_noalloc[NOALLOC_MAX_DEVICES];
+}  // namespace
+
+extern "C" {
+
+int lal_gpu_sample_noalloc(int batch, int vocab, const lal_gpu_sample_params *params,
+                           const lal_gpu_sample_io *io, void *stream)
+{
+    int dev = -1;
+    LAL_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= NOALLOC_MAX_DEVICES) return LAL_GPU_E_NODEV;
+    NoallocDevice &d = g_noalloc[dev];
+    std::call_once(d.once, [&]() {
+        NoallocScratch *ptr = nullptr;
+        hipError_t e = hipGetSymbolAddress((void **)&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr) {
+            d.rc = hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol);
+            return;
+        }
+        int ncu = 0;
+        if (hipDeviceGetAttribute(&ncu, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || ncu <= 0)
+            ncu = 256;
+        d.ncu = ncu;
+        if (const char *env = getenv("LAL_GPU_SLICES")) d.forced_slices = std::max(0, atoi(env));
+        hipLaunchKernelGGL(clear_u32_kernel, dim3((LAL_GPU_NOALLOC_MAX_ROWS + 255) / 256), dim3(256), 0,
+                           (hipStream_t)stream, ptr->arrive, LAL_GPU_NOALLOC_MAX_ROWS);
+        e = hipGetLastError();
+        if (e != hipSuccess) {
+            d.rc = hip_fail(e);
+            return;
+        }
+        d.ptr = ptr;
+    });
+    if (d.rc != LAL_GPU_OK || !d.ptr) return d.rc != LAL_GPU_OK ? d.rc : LAL_GPU_E_HIP;
+    if (batch > LAL_GPU_NOALLOC_MAX_ROWS && d.forced_slices > 1) return LAL_GPU_E_RANGE;
+    ListTarget t;
+    t.ncu = d.ncu;
+    t.forced_slices = d.forced_slices;
+    t.slice_rows = LAL_GPU_NOALLOC_MAX_ROWS;
+    t.lst_val = d.ptr->lst_val;
+    t.lst_idx = d.ptr->lst_idx;
+    t.lst_meta = d.ptr->lst_meta;
+    t.arrive = d.ptr->arrive;
+    return launch_sample(t, batch, vocab, params, io, stream);
+}
+
+int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_params *p,
+                   const lal_gpu_sample_io *io, void *stream)
+{
+    if (!ctx) return LAL_GPU_E_INVAL;
+    if (batch > ctx->max_batch || vocab > ctx->max_vocab) return LAL_GPU_E_RANGE;
+    ListTarget t;
+    t.ncu = ctx->ncu;
+    t.forced_slices = ctx->forced_slices;
+    t.slice_rows = ctx->max_batch;
+    t.lst_val = ctx->lst_val;
+    t.lst_idx = ctx->lst_idx;
+    t.lst_meta = ctx->lst_meta;
+    t.arrive = ctx->arrive;
+    return launch_sample(t, batch, vocab, p, io, stream);
 }
 
 int lal_gpu_sample_finish(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_params *p,
