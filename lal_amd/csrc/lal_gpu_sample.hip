@@ -570,6 +570,8 @@ struct WState {
     float tau;   // running lower bound of the row's k-th largest processed logit
     int strict;  // 1: buffer holds values > tau (more than CAPW tie at tau)
     int cnt;     // entries in the wave's buffer
+    float tcmp;  // the wave's own filter: values >= tcmp pass (next_up(tau)
+                 // when strict; nan, which nothing passes, above +inf)
 };
 
 // Wave radix select: k-th largest key over bv[0..cnt) and the lanes' values
@@ -745,40 +747,35 @@ __device__ __forceinline__ int wave_append(float *bv, int *bi, int base, const f
 // Offer this wave's values to its buffer: x[i] are upper bounds of the
 // processed logits (nan when out of range), tcmp the current filter.  On
 // overflow the wave resolves exact values (into a separate array), raises tau
-// to the k-th largest of buffer + offered values and compacts.  Element
-// e = eb[i/4] + i%4 is part of the row when 0 <= e < elim; a nan bound there
-// is a nan in the row and raises *nan_flag (padding lanes are nan as well).
+// to the k-th largest of buffer + offered values and compacts.  pm[i] is the
+// caller's ballot of x[i] >= tcmp: the masks come in as scalar values, so the
+// compiler never holds the comparisons as per-lane booleans across the call.
 // Wave-synchronous, no workgroup barrier.
 template <int NQ, int CAPW>
 __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, const RowCtx &R,
-                                           const float (&x)[4 * NQ],
-                                           const int (&eb)[NQ], int elim, float tcmp, WState &st, int k,
-                                           unsigned *tau_key_shared, int *nan_flag)
+                                           const float (&x)[4 * NQ], const unsigned long long (&pm)[4 * NQ],
+                                           const int (&eb)[NQ], float tcmp, WState &st, int k,
+                                           unsigned *tau_key_shared)
 {
     constexpr int NV = 4 * NQ;
     const int tag = R.use_hash ? UNREFINED : 0;
-    {
-        bool nan_here = false;
-#pragma unroll
-        for (int i = 0; i < NV; ++i) {
-            const int e = eb[i >> 2] + (i & 3);
-            nan_here |= (x[i] != x[i]) && e >= 0 && e < elim;
-        }
-        if (__ballot(nan_here) && lane_id() == 0) *nan_flag = 1;
-    }
     // append path: the per-slot ballots give the count (scalar popcounts) and
     // each lane's position (mbcnt); no cross-lane data exchange
     int total = 0;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) total += __popcll(__ballot(x[i] >= tcmp));
+    for (int i = 0; i < NV; ++i) total += __popcll(pm[i]);
     if (total == 0) return;
+    // the lanes' own tests go through an opaque copy of the filter, so that
+    // they are not merged with the caller's ballots
+    float tl = tcmp;
+    asm volatile("" : "+v"(tl));
     if (st.cnt + total <= CAPW) {
         int base = st.cnt;
 #pragma unroll
         for (int i = 0; i < NV; ++i) {
-            const unsigned long long mk = __ballot(x[i] >= tcmp);
+            const unsigned long long mk = pm[i];
             if (mk) {
-                if (x[i] >= tcmp) {
+                if (x[i] >= tl) {
                     const int pos = base + lanes_below(mk);
                     bv[pos] = x[i];
                     bi[pos] = (eb[i >> 2] + (i & 3)) | tag;
@@ -791,7 +788,7 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
     }
     uint32_t m = 0;
 #pragma unroll
-    for (int i = 0; i < NV; ++i) m |= (x[i] >= tcmp) ? (1u << i) : 0u;
+    for (int i = 0; i < NV; ++i) m |= (x[i] >= tl) ? (1u << i) : 0u;
     // overflow: exact values for the offered entries and the buffer
     float y[NV];
 #pragma unroll
@@ -851,6 +848,7 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
     if (tk != st.tau || strict != (bool)st.strict) {
         st.tau = tk;
         st.strict = strict ? 1 : 0;
+        st.tcmp = strict ? next_up(tk) : tk;
         if (lane_id() == 0) atomicMax(tau_key_shared, fkey(tk));
     }
 }
@@ -1895,6 +1893,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         st.tau = -INFINITY;
         st.strict = 0;
         st.cnt = 0;
+        st.tcmp = -INFINITY;
 
     // ---- stream: each wave owns its share, no workgroup barrier ----------
     if (w == 0 && has_extras) {
@@ -1903,8 +1902,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         float x[4] = {NAN, NAN, NAN, NAN};
         const int eb[1] = {e};
         if (e >= 0) x[0] = upper_bound<HAS_BIAS, HAS_ALLOW>(A.bias, abits, e, row[e]);
-        wave_offer<1, CAPW>(bv, bi, hist, R, x, eb, (e >= 0) ? e + 1 : 0, -INFINITY, st, k, &S.tau_key,
-                            &S.nan_flag);
+        if (__ballot(e >= 0 && x[0] != x[0]) && lane == 0) S.nan_flag = 1;
+        unsigned long long pm[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pm[i] = __ballot(x[i] >= -INFINITY);
+        wave_offer<1, CAPW>(bv, bi, hist, R, x, pm, eb, -INFINITY, st, k, &S.tau_key);
     }
     for (int q0 = qb; q0 < qe; q0 += WITER) {
         // two iterations stay in flight while this one is filtered
@@ -1923,12 +1925,10 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         // effective filter: own threshold, or the largest any wave of this
         // row has reached (each is a lower bound of the row's k-th largest);
         // a strict threshold becomes ">=" against the next float up
-        const unsigned tks = S.tau_key;
-        const float tsh = tks ? keyf(tks) : -INFINITY;
-        const bool own = st.tau >= tsh;
-        const float thr = own ? st.tau : tsh;
-        const bool sx = own && st.strict;
-        const float tcmp = sx ? next_up(thr) : thr;
+        // (keyf(0), "none", is a nan and drops out of the fmaxf; a nan own
+        // filter passes nothing and stays)
+        const float tsh = keyf(S.tau_key);
+        const float tcmp = (st.tcmp != st.tcmp) ? st.tcmp : fmaxf(st.tcmp, tsh);
         // processed-value upper bounds (values of invalid lanes are nan)
         float x[VPL];
 #pragma unroll
@@ -1965,17 +1965,31 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
 #pragma unroll
                     for (int c = 0; c < 4; ++c) x[4 * u + c] = NAN;
         }
-        // a value enters the offer when it passes the filter or is nan (a nan
-        // in the row, or a padding lane of a partial iteration)
-        unsigned long long any = 0ull;
+        // a nan never passes the filter; the row's nans are found here, two
+        // values per unordered compare (padding lanes of a partial
+        // iteration are nan too and stay out)
+        {
+            unsigned long long nanm = 0ull;
 #pragma unroll
-        for (int i = 0; i < VPL; ++i) any |= __ballot(!(x[i] < tcmp));
+            for (int u = 0; u < U4; ++u) {
+                unsigned long long nu = __ballot(__builtin_isunordered(x[4 * u], x[4 * u + 1])) |
+                                        __ballot(__builtin_isunordered(x[4 * u + 2], x[4 * u + 3]));
+                if (q0 + WITER > qe) nu &= __ballot(q0 + u * 64 + lane < qe);
+                nanm |= nu;
+            }
+            if (nanm && lane == 0) S.nan_flag = 1;
+        }
+        unsigned long long pm[VPL], any = 0ull;
+#pragma unroll
+        for (int i = 0; i < VPL; ++i) {
+            pm[i] = __ballot(x[i] >= tcmp);
+            any |= pm[i];
+        }
         if (any) {
             int eb[U4];
 #pragma unroll
             for (int u = 0; u < U4; ++u) eb[u] = g.head + 4 * (q0 + u * 64 + lane);
-            wave_offer<U4, CAPW>(bv, bi, hist, R, x, eb, g.head + 4 * qe, tcmp, st, k, &S.tau_key,
-                                 &S.nan_flag);
+            wave_offer<U4, CAPW>(bv, bi, hist, R, x, pm, eb, tcmp, st, k, &S.tau_key);
         }
 #pragma unroll
         for (int u = 0; u < U4; ++u) {
