@@ -25,6 +25,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0  # MI355X HBM3E, AMD published
+MIN_LIVE_BYTES = 512 << 20  # 2x the 256 MB Infinity Cache
 
 WORKLOADS = {
     # name: (batch, vocab, kind, T, k, top_p, penalty, history, extra)
@@ -173,53 +174,84 @@ def params_for(w):
                            flags=abi.F_DRAW_GPT2 if w.get("gpt2") else 0)
 
 
-def cpu_baseline(w, dev, inputs, target_s=4.0):
-    """The CPU oracle (C, OpenMP over rows) on the same bytes: a bounded
-    sample of the workload's rows, timed on this host's cores."""
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def host_threads():
+    try:
+        n = len(os.sched_getaffinity(0))
+    except AttributeError:
+        n = os.cpu_count() or 1
+    return int(os.environ.get("OMP_NUM_THREADS", n))
+
+
+def timed_median(fn, reps):
+    """Median wall time of fn() over reps runs (one untimed run first)."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    ts.sort()
+    return ts[len(ts) // 2]
+
+
+def cpu_baseline(w, dev, inputs, reps=20):
+    """The CPU oracle (C, OpenMP over rows) on the same bytes, timed on this
+    host's cores: a bounded sample of the step's rows spread over the batch
+    (every B/n-th row), the median of `reps` repetitions, with all threads
+    and with one."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_lib import Oracle, make_params as oparams
     orc = Oracle()
     B, V, H = w["B"], w["V"], w["H"]
-    nrows = min(B, 256)
-    x = inputs.logits.download((B, V), np.float32)[:nrows].copy()
-    h = inputs.hist.download((B, H), np.int32)[:nrows].copy()
-    u = inputs.u.download(B, np.float32)[:nrows].copy()
-    allow = inputs.allow.download((B, inputs.words), np.uint32)[:nrows].copy() if inputs.allow is not None else None
+    threads = host_threads()
+    x_all = inputs.logits.download((B, V), np.float32)
+    h_all = inputs.hist.download((B, H), np.int32)
+    u_all = inputs.u.download(B, np.float32)
+    a_all = inputs.allow.download((B, inputs.words), np.uint32) if inputs.allow is not None else None
     bias = inputs.bias.download(V, np.float32) if inputs.bias is not None else None
     p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"],
-                mask_recent=w.get("mask_recent", 0))
-    threads = os.cpu_count() or 1
-    try:
-        threads = len(os.sched_getaffinity(0))
-    except AttributeError:
-        pass
-    threads = int(os.environ.get("OMP_NUM_THREADS", threads))
+                mask_recent=w.get("mask_recent", 0), flags=2 if w.get("gpt2") else 0)
+    per_row = algorithmic_bytes_per_row(w)
 
-    def timed(nthreads, rows_target_s):
-        done, t0 = 0, time.perf_counter()
-        reps = 0
-        while True:
+    def measure(nthreads, nrows):
+        idx = np.linspace(0, B - 1, nrows).astype(np.int64) if nrows < B else np.arange(B)
+        x, h, u = x_all[idx].copy(), h_all[idx].copy(), u_all[idx].copy()
+        a = a_all[idx].copy() if a_all is not None else None
+
+        def run():
             xx = x.copy()  # the sampler penalises in place
-            orc.sample_batch(xx, p, hist=h, allow=allow, bias=bias, uniforms=u, nthreads=nthreads)
-            done += nrows
-            reps += 1
-            el = time.perf_counter() - t0
-            if el >= rows_target_s or reps >= 64:
-                return done / el, done
+            orc.sample_batch(xx, p, hist=h, allow=a, bias=bias, uniforms=u, nthreads=nthreads)
 
-    rows_s, done = timed(threads, target_s)
-    rows_s1, done1 = timed(1, target_s / 4)
+        t = timed_median(run, reps)
+        return len(idx) / t, len(idx)
+
+    rows_s, n_all = measure(threads, min(B, 32 * threads))
+    rows_s1, n_one = measure(1, min(B, 16))
     return {"value": rows_s, "unit": "rows/s", "cores": threads, "kind": "port",
-            "sample": f"{done} rows (first {nrows} rows of the step's batch, repeated), "
-                      f"OpenMP over rows; 1-thread: {rows_s1:.1f} rows/s over {done1} rows",
-            "one_thread_rows_per_s": rows_s1}
+            "gbs": rows_s * per_row / 1e9,
+            "sample": f"{n_all} rows spread over the batch, median of {reps} repetitions, OpenMP over rows "
+                      f"on {threads} threads ({cpu_model()}); 1 thread: {rows_s1:.1f} rows/s "
+                      f"({rows_s1 * per_row / 1e9:.2f} GB/s) over {n_one} rows",
+            "cpu_model": cpu_model(), "one_thread_rows_per_s": rows_s1,
+            "one_thread_gbs": rows_s1 * per_row / 1e9, "repetitions": reps}
 
 
-def cpu_baseline_lmhead(w, dev, inputs):
-    """The CPU oracle for one row of the Q8 LM head + sampling step: quantize
-    the hidden state, the int8 LM head over the full vocabulary (OpenMP over
-    vocab rows, as tools/server/qwen7b_server.c:833-845 splits it), then the
-    sampler; timed on this host's cores."""
+def cpu_baseline_lmhead(w, dev, inputs, reps=20):
+    """The CPU oracle for one row of the LM head + sampling step: quantize the
+    hidden state, the int8 LM head over the full vocabulary (OpenMP over
+    vocabulary rows, as tools/server/qwen7b_server.c:833-845 splits it), the
+    re-rank for GPT-2, then the sampler; the median of `reps` repetitions."""
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from oracle_lib import Oracle, make_params as oparams
     orc = Oracle()
@@ -230,25 +262,24 @@ def cpu_baseline_lmhead(w, dev, inputs):
     x = L["x"].download((w["B"], n), np.float32)[0].copy()
     h = inputs.hist.download((w["B"], w["H"]), np.int32)[:1].copy()
     u = inputs.u.download(w["B"], np.float32)[:1].copy()
-    p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"])
-    threads = int(os.environ.get("OMP_NUM_THREADS", len(os.sched_getaffinity(0))))
-    done, t0 = 0, time.perf_counter()
     gpt2 = bool(w.get("gpt2"))
-    if gpt2:
-        p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"], flags=2)
-    while True:
+    p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"],
+                flags=2 if gpt2 else 0)
+    threads = host_threads()
+
+    def run():
         sx, xq = orc.quantize_x(x, 1 if gpt2 else 0)
         logits = orc.lm_head(xq, sx, W, sw, nthreads=threads)
         if gpt2:
             orc.gpt2_rerank(logits, x, W, sw, w["rerank"])
         orc.sample_batch(logits[None, :], p, hist=h, uniforms=u, nthreads=1)
-        done += 1
-        el = time.perf_counter() - t0
-        if el >= 4.0 or done >= 32:
-            break
-    return {"value": done / el, "unit": "rows/s", "cores": threads, "kind": "port",
-            "sample": f"{done} rows (row 0 of the batch, repeated): quantize, LM head over "
-                      f"{V} x {n} int8 with OpenMP over vocab rows, "
+
+    t = timed_median(run, reps)
+    per_row = lm_head_weight_bytes(w) + 4 * n + 4 * w["H"] + 8
+    return {"value": 1.0 / t, "unit": "rows/s", "cores": threads, "kind": "port",
+            "gbs": per_row / t / 1e9, "cpu_model": cpu_model(), "repetitions": reps,
+            "sample": f"row 0 of the batch, median of {reps} repetitions on {threads} threads "
+                      f"({cpu_model()}): quantize, LM head over {V} x {n} int8 with OpenMP over vocabulary rows, "
                       f"{'re-rank of the top 512, ' if gpt2 else ''}sampler"}
 
 
@@ -272,7 +303,8 @@ def main():
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--workload", default="qwen7b_batched_topk_topp", choices=sorted(WORKLOADS))
-    ap.add_argument("--sets", type=int, default=2, help="rotating input sets")
+    ap.add_argument("--sets", type=int, default=0,
+                    help="rotating input sets (default: enough for 512 MiB of live inputs, at least 2)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--lm-head-layout", default="packed", choices=("packed", "rowmajor"),
                     help="weight layout of the Q8 LM head workloads")
@@ -289,7 +321,16 @@ def main():
     from lal_amd import abi
     w = WORKLOADS[args.workload]
     dev = abi.Device(0, max_batch=w["B"], max_vocab=w["V"])
-    nsets = 1 if w["kind"] in ("lmhead", "gpt2lm") else max(1, args.sets)  # W dominates the footprint
+    # Inputs rotate over at least 2x the 256 MB Infinity Cache, so that HBM
+    # and not the cache serves them (the LM head workloads' W alone is larger).
+    set_bytes = 4 * w["B"] * w["V"] + (4 * w["B"] * ((w["V"] + 31) // 32) if w.get("allow") else 0)
+    if w["kind"] in ("lmhead", "gpt2lm"):
+        nsets = 1
+    elif args.sets > 0:
+        nsets = args.sets
+    else:
+        # (a single row is latency-bound: 32 sets, cache-resident, are enough)
+        nsets = min(32, max(2, -(-MIN_LIVE_BYTES // set_bytes)))
     sets = [Inputs(dev, w, 1000 + 17 * i, packed=args.lm_head_layout == "packed") for i in range(nsets)]
     ios = [s.io(w) for s in sets]
     params = params_for(w)
@@ -357,7 +398,8 @@ def main():
                    **({"hidden": w["n"], "lm_head": "int8 [50257, 768] + per-row fp32 scales, top 512 "
                        "re-scored in fp32", "draw": "gpt2"} if w["kind"] == "gpt2lm" else {}),
                    "rotating_input_sets": len(sets),
-                   "live_input_bytes": len(sets) * 4 * w["B"] * w["V"],
+                   "live_input_bytes": (lm_head_weight_bytes(w) if w["kind"] in ("lmhead", "gpt2lm")
+                                        else len(sets) * set_bytes),
                    **({"allow_p": w["allow"], "bias_nnz": w["bias_nnz"],
                        "mask_recent": w["mask_recent"]} if w.get("allow") else {})},
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
