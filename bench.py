@@ -56,6 +56,10 @@ for _b in (1, 16):
                                                    top_p=0.0, pen=1.2, H=128, gpt2=True, rerank=512)
 
 
+DOMINANT = {"lmhead": "lm_head_packed_xres_kernel (B <= 16) / lm_head_packed_kernel",
+            "gpt2lm": "lm_head_dot4_kernel + rerank_select_kernel"}
+
+
 def lm_head_weight_bytes(w):
     return w["V"] * w["n"] + 4 * w["V"]
 
@@ -306,6 +310,8 @@ def main():
     ap.add_argument("--sets", type=int, default=0,
                     help="rotating input sets (default: enough for 512 MiB of live inputs, at least 2)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--lm-head-step", default="fused", choices=("fused", "composed"),
+                    help="Q8 LM head workloads: lal_gpu_lm_head_sample (fused) or quantize + head + sampler calls")
     ap.add_argument("--lm-head-layout", default="packed", choices=("packed", "rowmajor"),
                     help="weight layout of the Q8 LM head workloads")
     args = ap.parse_args()
@@ -337,6 +343,16 @@ def main():
 
     def step(i):
         inp = sets[i % len(sets)]
+        if inp.lmhead is not None and not inp.lmhead.get("gpt2") and inp.lmhead["wpk"] is not None \
+                and args.lm_head_step == "fused":
+            # one call: quantize, packed head (with candidate lists), sampler
+            L = inp.lmhead
+            io = ios[i % len(ios)]
+            abi.check(dev.lib.lal_gpu_lm_head_sample(dev.ctx, abi.ptr(L["x"]), w["B"], L["n"], abi.ptr(L["xq"]),
+                                                     abi.ptr(L["sx"]), abi.ptr(L["wpk"]), abi.ptr(L["sw"]), w["V"],
+                                                     abi.ptr(inp.logits), w["V"], C.byref(params), C.byref(io),
+                                                     dev.stream), "lm_head_sample")
+            return
         if inp.lmhead is not None:
             L = inp.lmhead
             abi.check(dev.lib.lal_gpu_quantize_x(dev.ctx, abi.ptr(L["x"]), w["B"], L["n"],
@@ -405,7 +421,8 @@ def main():
         "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": achieved / HBM_PEAK_GBS, "traffic": traffic,
                      "algorithmic_bytes_per_launch": bytes_step,
-                     "kernel": "sample_rows_kernel", "avg_launch_ms": ms_step},
+                     "kernel": DOMINANT.get(w["kind"], "sample_rows_kernel"), "avg_launch_ms": ms_step,
+                     "timed": "whole step (every launch of the step), HIP events on its stream"},
         "wall_s_timed_region": wall,
     }
     if not args.no_cpu_baseline:

@@ -201,10 +201,13 @@ int  lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab,
  * on the first call on each device.  Batches of up to that many rows are
  * sliced as lal_gpu_sample slices them; larger batches run one workgroup per
  * row and use no scratch (results never depend on slicing).  A forced slice
- * count (LAL_GPU_SLICES) with a larger batch is LAL_GPU_E_RANGE.  Every call
+ * count (LAL_GPU_SLICES) with a larger batch is LAL_GPU_E_RANGE.  A call with
+ * a bias keeps the bias's nonzero map in the same array, for vocabularies of
+ * up to LAL_GPU_NOALLOC_MAX_BIAS_VOCAB ids (larger: LAL_GPU_E_RANGE).  Every call
  * on one GPU shares that GPU's scratch: calls that overlap on one GPU (two
  * streams, two threads) race; calls in one stream order are safe. */
 #define LAL_GPU_NOALLOC_MAX_ROWS 64
+#define LAL_GPU_NOALLOC_MAX_BIAS_VOCAB (1 << 20)
 int  lal_gpu_sample_noalloc(int batch, int vocab, const lal_gpu_sample_params *params,
                             const lal_gpu_sample_io *io, void *stream);
 
@@ -239,6 +242,27 @@ int  lal_gpu_pack_q8(lal_gpu_ctx *ctx, const int8_t *d_w, int vocab, int n, int8
 int  lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float *d_sx,
                                int batch, int n, const int8_t *d_wpk, const float *d_sw,
                                int vocab, float *d_logits, int ld, void *stream);
+
+/* One decode step's LM head and token choice (tools/server/qwen7b_server.c:
+ * 829-848: lal_quantize_x, lal_lm_head_q8 over every vocabulary row, then the
+ * sampler): d_x [batch][n] fp32 -> d_xq / d_sx (quantize_x mode 0, also
+ * outputs) -> logits over the packed head into d_logits [batch][ld] -> the
+ * sampler with params / io (io->logits and io->ld are ignored: the step's
+ * logits are used).  Results are bit for bit those of lal_gpu_quantize_x +
+ * lal_gpu_lm_head_q8_packed + lal_gpu_sample.  For up to 16 rows without a
+ * bias or allow mask the head also keeps, per row, the logits at or above a
+ * bound taken from a fixed sample of its tiles, and the sampler reads that
+ * list instead of the row; a row whose list cannot be shown to hold its
+ * top-k pool (fewer than k values at or above the bound, a nan logit, a full
+ * list) is read whole, as lal_gpu_sample reads it.  LAL_GPU_LIST_KS (read
+ * when the context is created) overrides the bound's rank, for tests.
+ * Needs n % 16 == 0, 16-byte aligned d_xq / d_wpk, batch <= max_batch and
+ * vocab <= max_vocab of the context. */
+int  lal_gpu_lm_head_sample(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
+                            int8_t *d_xq, float *d_sx, const int8_t *d_wpk,
+                            const float *d_sw, int vocab, float *d_logits, int ld,
+                            const lal_gpu_sample_params *params,
+                            const lal_gpu_sample_io *io, void *stream);
 
 /* GPT-2 int8 LM head, pass 2 (tools/server/gpt2_server.c:2155-2215): d_logits
  * holds pass 1 (lal_gpu_lm_head_q8 over wte rows quantized by

@@ -93,6 +93,7 @@ EXPORTS = [
     ("lal_gpu_load_lm_head", _i, [_vp, _vp, C.c_char_p, _vp, _vp, C.POINTER(_i), C.POINTER(_i), _vp]),
     ("lal_gpu_pack_q8", _i, [_vp, _vp, _i, _i, _vp, _vp]),
     ("lal_gpu_lm_head_q8_packed", _i, [_vp, _vp, _vp, _i, _i, _vp, _vp, _i, _vp, _i, _vp]),
+    ("lal_gpu_lm_head_sample", _i, [_vp, _vp, _i, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _vp, _vp, _vp]),
     ("lal_gpu_uniforms_rand", None, [_u, _i, C.POINTER(_f), _i]),
     ("lal_gpu_malloc", _i, [C.POINTER(_vp), _sz]),
     ("lal_gpu_free", _i, [_vp]),
@@ -218,8 +219,12 @@ class Device:
 
     def close(self):
         if self.ctx:
+            self.lib.lal_gpu_stream_sync(self.stream)
             self.lib.lal_gpu_destroy(self.ctx)
             self.ctx = None
+        if self.stream:
+            self.lib.lal_gpu_stream_destroy(self.stream)
+            self.stream = None
 
     def sample(self, batch, vocab, params, io):
         check(self.lib.lal_gpu_sample(self.ctx, batch, vocab, C.byref(params), C.byref(io),

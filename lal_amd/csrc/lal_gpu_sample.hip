@@ -29,6 +29,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cmath>
 #include <climits>
 #include <mutex>
 #include <math.h>
@@ -60,6 +61,7 @@ constexpr int CAPW_LARGE = 2048;
 constexpr int K_SMALL_MAX = 128;
 constexpr int MAX_SLICES = 64;                 // slices per row
 constexpr int FLAT_MAX = NWAVE * CAPW_LARGE;   // slice-list entries per row
+constexpr int HMETA_STRIDE = 16;               // int4 per row of an LM head's list state (256 bytes)
 // row sample for the threshold estimate: 64 float4 (1 KB) every SBLK float4
 constexpr int SBLK = 2048;          // 32 KB stride -> 1/32 of the row
 constexpr int SR = 5;               // float4 per thread: up to 20 sampled blocks (V <= 163840 fully sampled)
@@ -246,6 +248,7 @@ struct Smem {
     int walive[NWAVE];    // live entries
     unsigned tau_key;     // max over the waves' thresholds (order-preserving key)
     int nan_flag;         // the row holds a nan processed value
+    unsigned bias_key;    // key of the largest flagged bias entry (all ones: a nan or -inf)
     float wtau[NWAVE];
     int wstrict[NWAVE];
     int wsum[2][NWAVE];
@@ -270,6 +273,9 @@ struct KArgs {
     const uint32_t *allow;
     int allow_ld;
     const float *bias;
+    const uint32_t *bias_bits;  // bit e set unless bias[e] is +0.0 (bias_prep_kernel)
+    const uint32_t *bias_part;  // per-block maximum keys of the flagged bias entries
+    int bias_nparts;            // <= WG
     const float *uniforms;
     int *out_token;
     float *out_thr;
@@ -304,6 +310,15 @@ struct KArgs {
     int *lst_idx;       // [batch][nslice][lcap] candidate ids
     int4 *lst_meta;     // [batch][nslice] (count, threshold bits, strict, -)
     unsigned *arrive;   // [batch] slices finished; reset by the finisher
+    // candidate lists an LM head wrote (list mode): row b's entries at
+    // lst_val / lst_idx + b * hcap, hmeta[b * HMETA_STRIDE] = (count, -, -,
+    // flags: 1 list full, 2 a nan logit), hslots[b][64] the sample slots the
+    // bound comes from (rank hks); both are cleared by the row's workgroup for
+    // the next head
+    int4 *hmeta;
+    unsigned *hslots;
+    int hcap;
+    int hks;            // rank of the head's bound among the 64 slots
     int ncu;            // compute units: workgroups [3*ncu, 4*ncu) are the
                         // fourth (youngest) resident on their CU
 };
@@ -505,6 +520,17 @@ __device__ __forceinline__ int extra_elem(const RowGeo &g, int t)
     return -1;
 }
 
+// Bits [rel, rel + 4) of a bitmap window spread over the wave, one word per
+// lane (lane i: word i); two words when the bits may straddle a word edge.
+__device__ __forceinline__ uint32_t window_nibble(uint32_t word, int rel, bool two)
+{
+    const int wi = rel >> 5;
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(wi << 2, (int)word);
+    if (!two) return (lo >> (rel & 31)) & 0xFu;
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute((wi + 1) << 2, (int)word);
+    return (uint32_t)((((uint64_t)hi << 32) | lo) >> (rel & 31)) & 0xFu;
+}
+
 // cheap upper bound of the processed logit: raw + bias, -inf if not allowed
 template <bool HAS_BIAS, bool HAS_ALLOW>
 __device__ __forceinline__ float upper_bound(const float *bias, const uint32_t *abits, int e, float x)
@@ -528,14 +554,16 @@ struct RowCtx {
     const int *hinfo;
     float pen;
     bool has_bias, has_allow, use_hash;
+    bool bound_bias;  // bounds may carry the bias maximum in place of bias[e]
 };
 
 // exact value of id e from its upper bound yhat, given its hash slot s (-1:
-// not in the hash, and the bound is exact)
+// not in the hash, and the bound is exact unless it may carry the bias
+// maximum)
 __device__ __forceinline__ float exact_at_slot(const RowCtx &R, int e, float yhat, int s)
 {
-    if (s < 0) return yhat;
-    const int info = R.hinfo[s];
+    if (s < 0 && !R.bound_bias) return yhat;
+    const int info = (s >= 0) ? R.hinfo[s] : 0;
     // without a bias the upper bound is the raw logit (or -inf when the allow
     // bit is clear, which the mask below keeps)
     const float raw = R.has_bias ? R.row[e] : yhat;
@@ -758,7 +786,7 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
                                            unsigned *tau_key_shared)
 {
     constexpr int NV = 4 * NQ;
-    const int tag = R.use_hash ? UNREFINED : 0;
+    const int tag = (R.use_hash || R.bound_bias) ? UNREFINED : 0;
     // append path: the per-slot ballots give the count (scalar popcounts) and
     // each lane's position (mbcnt); no cross-lane data exchange
     int total = 0;
@@ -800,7 +828,7 @@ __device__ __forceinline__ void wave_offer(float *bv, int *bi, unsigned *hist, c
         }
     }
     wave_sync();
-    if (R.use_hash) wave_refine(bv, bi, st.cnt, R, st.tau, st.strict);
+    if (R.use_hash || R.bound_bias) wave_refine(bv, bi, st.cnt, R, st.tau, st.strict);
     int cnt = wave_compact(bv, bi, st.cnt, st.tau, st.strict);
     const int offered = wave_sum(__popc(m));
     float tk = st.tau;
@@ -1019,6 +1047,7 @@ __device__ __forceinline__ float rescan_value(const KArgs &A, const SM &S, const
     R.has_bias = HAS_BIAS;
     R.has_allow = HAS_ALLOW;
     R.use_hash = use_hash;
+    R.bound_bias = false;
     return exact_value(R, e, yh);
 }
 
@@ -1695,8 +1724,10 @@ __device__ __forceinline__ RowResult block_epilogue(const KArgs &A, SM &S, int n
 // ---------------------------------------------------------------------------
 // The sampler kernel: one workgroup (four wave64) per row.
 // ---------------------------------------------------------------------------
-template <bool HAS_BIAS, bool HAS_ALLOW, int CAPW>
-__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void sample_rows_kernel(KArgs A)
+// LIST: list mode (an LM head's candidate lists), at most 16 rows of one
+// workgroup each, so no occupancy target
+template <bool HAS_BIAS, bool HAS_ALLOW, int CAPW, bool LIST = false>
+__global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4, 8))) void sample_rows_kernel(KArgs A)
 {
     __shared__ Smem<CAPW> S;
     constexpr int PER = NWAVE * CAPW / WG;  // union entries per thread
@@ -1738,6 +1769,19 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     const int bid = (tid < A.n_ban) ? A.ban_ids[tid] : -1;
     const int last_tok = (A.last_tokens && A.ban_last) ? A.last_tokens[b] : -1;
     const uint64_t xtab = (tid < 32) ? kExp2Tab[tid] : 0ull;
+    const uint32_t bpk = (HAS_BIAS && tid < A.bias_nparts) ? A.bias_part[tid] : 0u;
+    // list mode: the row's candidates are complete when the list holds at
+    // least k values above the largest bound the head filtered with (checked
+    // after the list pass); a full list, a nan logit or no bound: the row is
+    // streamed
+    int hcnt = 0;
+    uint32_t hkey = 0u;
+    bool list_ok = false;
+    if (LIST) {
+        const int4 hm = A.hmeta[(size_t)b * HMETA_STRIDE];
+        hcnt = hm.x;
+        list_ok = (hm.w & 3) == 0 && hcnt >= 0 && hcnt <= A.hcap;
+    }
 
     const RowGeo g = row_geo(row, V);
     const int k = A.greedy ? 1 : min(max(A.k, 1), V);
@@ -1750,18 +1794,34 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     const bool has_extras = (sl == 0) && (g.head + g.ntail > 0);
     const int vlen = 4 * (se - sb) + (has_extras ? g.head + g.ntail : 0);
     const f32x4 *row4 = reinterpret_cast<const f32x4 *>(row + g.head);
+    // allow and bias-nonzero bits: lane l holds word l of the 34 words under
+    // a wave-iteration (the window starts at the word of its first element)
+    const int nwords = (V + 31) >> 5;
+    auto wload = [&](const uint32_t *bits, int q) -> uint32_t {
+        const int wi = ((g.head + 4 * q) >> 5) + lane;
+        return (lane < 34 && wi < nwords) ? bits[wi] : 0u;
+    };
+    uint32_t aw0 = 0u, aw1 = 0u, bw0 = 0u, bw1 = 0u;
 
     f32x4 cur[U4], nx1[U4];
     // few workgroups (a small batch): the first two stream iterations go out
     // with the sample, nothing queues behind them
     const bool early = A.batch <= 16;
-    if (early) {
+    if (early && !LIST) {
 #pragma unroll
         for (int u = 0; u < U4; ++u) {
             const int q = qb + u * 64 + lane;
             cur[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
             const int q1 = qb + WITER + u * 64 + lane;
             nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
+        }
+        if (HAS_ALLOW) {
+            aw0 = wload(abits, qb);
+            aw1 = wload(abits, qb + WITER);
+        }
+        if (HAS_BIAS) {
+            bw0 = wload(A.bias_bits, qb);
+            bw1 = wload(A.bias_bits, qb + WITER);
         }
     }
     // the slice sample goes out first, alone: every workgroup waits for its
@@ -1771,7 +1831,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     for (int r = 0; r < SR; ++r) {
         const int sidx = tid + WG * r;
         const int q = sb + (sidx >> 6) * SBLK + (sidx & 63);
-        smp[r] = (q < se) ? row4[q] : f32x4{NAN, NAN, NAN, NAN};
+        smp[r] = (q < se && !LIST) ? row4[q] : f32x4{NAN, NAN, NAN, NAN};
     }
 
     // ---- setup: hash of history / ban ids, and the threshold estimate ----
@@ -1789,7 +1849,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     }
     const float lam = (float)k * (float)nsmp / (float)max(vlen, 1);
     const int ks = (int)ceilf(lam + 6.0f * sqrtf(lam) + 6.0f);
-    const bool use_est = !A.greedy && nsmp > 0 && ks <= 64;
+    const bool use_est = !LIST && !A.greedy && nsmp > 0 && ks <= 64;
     {
         float lm = -INFINITY;
 #pragma unroll
@@ -1806,7 +1866,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         skeys[tid] = (lm == lm && lm > -INFINITY) ? fkey(lm) : 0u;
     }
     // the first two iterations' loads fly during the hash setup and estimate
-    if (!early) {
+    if (!early && !LIST) {
 #pragma unroll
         for (int u = 0; u < U4; ++u) {
             const int q = qb + u * 64 + lane;
@@ -1814,14 +1874,29 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             const int q1 = qb + WITER + u * 64 + lane;
             nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
         }
+        if (HAS_ALLOW) {
+            aw0 = wload(abits, qb);
+            aw1 = wload(abits, qb + WITER);
+        }
+        if (HAS_BIAS) {
+            bw0 = wload(A.bias_bits, qb);
+            bw1 = wload(A.bias_bits, qb + WITER);
+        }
     }
     for (int s = tid; s < HSLOTS; s += WG) {
         S.hkey[s] = -1;
         S.hinfo[s] = 0;
     }
     if (tid < 32) S.exptab[tid] = xtab;
-    if (tid == 0) S.nan_flag = 0;
+    if (tid == 0) {
+        S.nan_flag = 0;
+        S.bias_key = 0u;
+    }
     __syncthreads();
+    if (HAS_BIAS) {
+        const uint32_t m = wave_max_u(bpk);
+        if (lane == 0) atomicMax(&S.bias_key, m);
+    }
 #pragma unroll
     for (int r = 0; r < 2; ++r) {
         const int i = tid + r * WG;
@@ -1854,6 +1929,22 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const uint32_t kk = (uint32_t)S.sel_rem;
         if (kk) tau_est = keyf(kk);
     }
+    if (LIST) {
+        // the head's bound from the final slots (at least every bound a wave
+        // filtered with, so the list holds every value at or above it)
+        if (w == 0) {
+            const uint32_t K = wave_kth_lane_key(A.hslots[(size_t)b * 64 + lane], A.hks);
+            if (lane == 0) S.sel_rem = (int)K;
+        }
+        __syncthreads();
+        hkey = (uint32_t)S.sel_rem;
+        __syncthreads();
+        if (hkey == 0u) list_ok = false;
+        if (list_ok) tau_est = keyf(hkey);
+    }
+    // bound of bias[e] for a set bias bit (a nan when one flagged entry is a
+    // nan or -inf: those rows take the nan path, which reads the bias itself)
+    const float bmax = HAS_BIAS ? keyf(S.bias_key) : 0.0f;
     const bool use_hash = (nh > 0) || (A.n_ban > 0);
     RowCtx R;
     R.row = row;
@@ -1865,14 +1956,19 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     R.has_bias = HAS_BIAS;
     R.has_allow = HAS_ALLOW;
     R.use_hash = use_hash;
+    R.bound_bias = HAS_BIAS;
 
     float *bv = S.cval + w * CAPW;
     int *bi = S.cidx + w * CAPW;
     unsigned *hist = S.u.h.whist[w];
-    const bool bias_vec = HAS_BIAS && ((((uintptr_t)(A.bias + g.head)) & 15) == 0);
+    // a lane's 4 bits of a window can straddle two words unless the row's
+    // aligned body starts on a multiple of 4 elements
+    const bool two_words = g.head != 0;
     WState st;
     for (int attempt = 0; attempt < 2; ++attempt) {
-        if (attempt == 1) {
+        // list mode: the first pass reads the head's list, not the row
+        const bool from_list = LIST && list_ok && attempt == 0;
+        if (attempt == 1 || (LIST && !list_ok)) {
             // the estimate was above the row's k-th largest: stream again.  The
             // share's start goes through an opaque copy, so that the compiler
             // recomputes these loads' masks and addresses here instead of
@@ -1886,6 +1982,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
                 const int q1 = qa + WITER + u * 64 + lane;
                 nx1[u] = (q1 < qe) ? __builtin_nontemporal_load(row4 + q1) : f32x4{NAN, NAN, NAN, NAN};
             }
+            if (HAS_ALLOW) {
+                aw0 = wload(abits, qa);
+                aw1 = wload(abits, qa + WITER);
+            }
+            if (HAS_BIAS) {
+                bw0 = wload(A.bias_bits, qa);
+                bw1 = wload(A.bias_bits, qa + WITER);
+            }
         }
         __syncthreads();
         if (tid == 0) S.tau_key = (tau_est > -INFINITY) ? fkey(tau_est) : 0u;
@@ -1895,6 +1999,25 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         st.cnt = 0;
         st.tcmp = -INFINITY;
 
+    if (from_list) {
+        // every list value is a raw logit of an id the head computed once;
+        // the waves take 64 entries at a time, in rotation
+        const float *lv = A.lst_val + (size_t)b * A.hcap;
+        const int *li = A.lst_idx + (size_t)b * A.hcap;
+        for (int j0 = w * 64; j0 < hcnt; j0 += NWAVE * 64) {
+            const int j = j0 + lane;
+            float x[4] = {NAN, NAN, NAN, NAN};
+            int eb[1] = {0};
+            if (j < hcnt) {
+                x[0] = lv[j];
+                eb[0] = li[j];
+            }
+            const float tsh = keyf(S.tau_key);
+            const float tcmp = (st.tcmp != st.tcmp) ? st.tcmp : fmaxf(st.tcmp, tsh);
+            unsigned long long pm[4] = {__ballot(x[0] >= tcmp), 0ull, 0ull, 0ull};
+            if (pm[0]) wave_offer<1, CAPW>(bv, bi, hist, R, x, pm, eb, tcmp, st, k, &S.tau_key);
+        }
+    } else {
     // ---- stream: each wave owns its share, no workgroup barrier ----------
     if (w == 0 && has_extras) {
         // head / tail elements outside the aligned body (slice 0)
@@ -1911,6 +2034,8 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
     for (int q0 = qb; q0 < qe; q0 += WITER) {
         // two iterations stay in flight while this one is filtered
         f32x4 nx2[U4];
+        const uint32_t aw2 = HAS_ALLOW ? wload(abits, q0 + 2 * WITER) : 0u;
+        const uint32_t bw2 = HAS_BIAS ? wload(A.bias_bits, q0 + 2 * WITER) : 0u;
         if (q0 + 3 * WITER <= qe) {
 #pragma unroll
             for (int u = 0; u < U4; ++u)
@@ -1930,29 +2055,19 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         const float tsh = keyf(S.tau_key);
         const float tcmp = (st.tcmp != st.tcmp) ? st.tcmp : fmaxf(st.tcmp, tsh);
         // processed-value upper bounds (values of invalid lanes are nan)
+        // (a set bias bit adds the bias maximum: an upper bound, resolved
+        // from bias[e] when the entry is refined; a clear one adds +0.0, which
+        // is bias[e] itself)
         float x[VPL];
 #pragma unroll
         for (int u = 0; u < U4; ++u) {
-            const int e0 = g.head + 4 * (q0 + u * 64 + lane);
-            f32x4 bb = {0.0f, 0.0f, 0.0f, 0.0f};
-            if (HAS_BIAS) {
-                if (bias_vec) {
-                    bb = *reinterpret_cast<const f32x4 *>(A.bias + min(e0, V - 4));
-                } else {
-#pragma unroll
-                    for (int c = 0; c < 4; ++c) bb[c] = A.bias[min(e0 + c, V - 1)];
-                }
-            }
-            uint32_t ab = 0xFu;
-            if (HAS_ALLOW) {
-                const int ea = min(e0, V - 4 >= 0 ? V - 4 : 0);
-                const uint64_t w2 = ((uint64_t)abits[min(ea + 3, V - 1) >> 5] << 32) | abits[ea >> 5];
-                ab = (uint32_t)(w2 >> (ea & 31)) & 0xFu;
-            }
+            const int rel = ((g.head + 4 * q0) & 31) + 256 * u + 4 * lane;
+            const uint32_t ab = HAS_ALLOW ? window_nibble(aw0, rel, two_words) : 0xFu;
+            const uint32_t bb = HAS_BIAS ? window_nibble(bw0, rel, two_words) : 0u;
 #pragma unroll
             for (int c = 0; c < 4; ++c) {
                 float v = cur[u][c];
-                if (HAS_BIAS) v = v + bb[c];
+                if (HAS_BIAS) v = v + (((bb >> c) & 1u) ? bmax : 0.0f);
                 if (HAS_ALLOW && !((ab >> c) & 1u)) v = -INFINITY;
                 x[4 * u + c] = v;
             }
@@ -1996,10 +2111,15 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
             cur[u] = nx1[u];
             nx1[u] = nx2[u];
         }
+        aw0 = aw1;
+        aw1 = aw2;
+        bw0 = bw1;
+        bw1 = bw2;
     }
+    }  // stream
     // resolve the entries still holding upper bounds (below the estimate:
     // dropped, so the count below verifies it)
-    if (use_hash) wave_refine_batched(bv, bi, st.cnt, R, tau_est, false);
+    if (use_hash || HAS_BIAS) wave_refine_batched(bv, bi, st.cnt, R, tau_est, false);
     int alive = 0;
     uint32_t kx = 0u, kn = 0xFFFFFFFFu;  // range of the live keys
     for (int j = lane; j < st.cnt; j += 64) {
@@ -2033,6 +2153,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         tau_est = -INFINITY;
     }
     }  // attempt
+    if (LIST) {
+        // the head's per-row state starts from zero at its next launch
+        if (tid < 64) A.hslots[(size_t)b * 64 + tid] = 0u;
+        if (tid == 0) A.hmeta[(size_t)b * HMETA_STRIDE] = int4{0, 0, 0, 0};
+    }
 
     // Past the stream.  The arguments are read again from the kernel argument
     // segment through an opaque pointer, so that the fields the rest of the
@@ -2291,6 +2416,13 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(4, 8))) void
         // k = 1 selection below is exact
         T = NAN;
         forced_token = 0;
+        rescan = true;
+    } else if (HAS_BIAS && nan_row) {
+        // a nan bias maximum makes every flagged entry's stream bound a nan,
+        // so the buffers can lack the row's maximum: the scan's best is the
+        // root of a one-entry heap fed in id order (id 0 is not a nan here,
+        // and a nan never replaces the root), found over the exact values
+        T = heap_replay_threshold<HAS_BIAS, HAS_ALLOW>(A, S, R, 1);
         rescan = true;
     } else if (total >= k) {
         uint32_t kn, kx;
@@ -2629,29 +2761,99 @@ __global__ __launch_bounds__(WG) void finish_rows_kernel(FinishArgs F)
 // ---------------------------------------------------------------------------
 // int8 LM head front end (runtime/lal_q8_kernel.h:375-543)
 // ---------------------------------------------------------------------------
+// x86 float -> int32 conversion as the reference's builds execute it
+// (cvtps2dq rounds to nearest even, a C cast truncates): a nan or a value
+// outside the int32 range gives INT_MIN
+__device__ __forceinline__ int x86_cvt(float v, bool round_even)
+{
+    if (!(v >= -2147483648.0f && v < 2147483648.0f)) return INT_MIN;
+    return round_even ? (int)__builtin_rintf(v) : (int)v;
+}
+
+// _mm_max_ps: the first operand if it is greater, else the second
+__device__ __forceinline__ float x86_maxps(float a, float b) { return (a > b) ? a : b; }
+
 __global__ __launch_bounds__(256) void quantize_x_kernel(const float *x, int n, int mode,
                                                          int8_t *xq, float *sx)
 {
+    // mode 0 (AVX2 build): lane j of the 8-wide maximum sees |x[8c + j]| in
+    // chunk order; a nan there is kept only while no later value of the lane
+    // follows, so thread (segment s, lane j) folds its run of chunks into
+    // (nan seen, ends in nan, maximum after its last nan) and lane j's 32
+    // runs are folded in order.  mode 1: `a > max` over all values, which
+    // never takes a nan.
+    __shared__ float seg_m[256];
+    __shared__ int seg_f[256];
     __shared__ float red[4];
-    const int b = blockIdx.x;
+    const int b = blockIdx.x, t = threadIdx.x;
     const float *xr = x + (size_t)b * n;
+    const int n8 = (mode == 0) ? (n & ~7) : 0;
     float m = 0.0f;
-    for (int i = threadIdx.x; i < n; i += 256) m = fmaxf(m, fabsf(xr[i]));
-    m = wave_max(m);
-    if (lane_id() == 0) red[wave_id()] = m;
-    __syncthreads();
-    m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    if (mode == 0) {
+        const int j = t & 7, sgi = t >> 3, nch = n8 >> 3;
+        const int c0 = (int)(((long long)nch * sgi) / 32), c1 = (int)(((long long)nch * (sgi + 1)) / 32);
+        float acc = -1.0f;  // -1: no value after the last nan
+        int f = 0;          // 1: a nan seen, 2: the run ends in a nan, 4: the run has values
+        for (int c = c0; c < c1; ++c) {
+            const float a = fabsf(xr[8 * c + j]);
+            if (a != a) {
+                f = 1 | 2 | 4;
+                acc = -1.0f;
+            } else {
+                f = (f & 1) | 4;
+                acc = fmaxf(acc, a);
+            }
+        }
+        seg_m[t] = acc;
+        seg_f[t] = f;
+        __syncthreads();
+        if (t < 8) {
+            float la = -1.0f;
+            int lf = 0;
+            for (int sg = 0; sg < 32; ++sg) {
+                const int ff = seg_f[sg * 8 + t];
+                if (!(ff & 4)) continue;
+                if (ff & 1) {
+                    lf = ff;
+                    la = seg_m[sg * 8 + t];
+                } else {
+                    lf = (lf & 1) | 4;
+                    la = fmaxf(la, seg_m[sg * 8 + t]);
+                }
+            }
+            seg_m[t] = (lf & 2) ? __builtin_nanf("") : fmaxf(la, 0.0f);
+        }
+        __syncthreads();
+        if (t == 0) {
+            float h[4];
+            for (int q = 0; q < 4; ++q) h[q] = x86_maxps(seg_m[q], seg_m[q + 4]);
+            const float s1[4] = {h[2], h[3], h[0], h[1]};
+            for (int q = 0; q < 4; ++q) h[q] = x86_maxps(h[q], s1[q]);
+            float mm = x86_maxps(h[0], h[1]);
+            for (int i = n8; i < n; ++i) {
+                const float a = fabsf(xr[i]);
+                if (a > mm) mm = a;
+            }
+            red[0] = mm;
+        }
+        __syncthreads();
+        m = red[0];
+    } else {
+        for (int i = t; i < n; i += 256) m = fmaxf(m, fabsf(xr[i]));
+        m = wave_max(m);
+        if (lane_id() == 0) red[wave_id()] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    }
     float scale = m / 127.0f;
     if (scale < 1e-8f) scale = 1e-8f;
     const float inv = 1.0f / scale;
-    const int rne_end = (mode == 0) ? (n & ~7) : 0;
-    for (int i = threadIdx.x; i < n; i += 256) {
-        const float s = xr[i] * inv;
-        int q = (i < rne_end) ? (int)__builtin_rintf(s) : (int)s;
+    for (int i = t; i < n; i += 256) {
+        int q = x86_cvt(xr[i] * inv, i < n8);
         q = min(127, max(-127, q));
         xq[(size_t)b * n + i] = (int8_t)q;
     }
-    if (threadIdx.x == 0) sx[b] = scale;
+    if (t == 0) sx[b] = scale;
 }
 
 // GEMV/GEMM-by-rows: each wave computes LMH_ROWS vocab rows for all batch rows
@@ -3059,16 +3261,75 @@ __global__ __launch_bounds__(256) void quantize_w_kernel(const float *w, int n, 
 // rotation of lm_head_packed_kernel, block kb per 64 k-bytes), so each wave
 // streams its tiles' W with three steps in flight and no barrier per step.
 // Same arithmetic as lm_head_packed_kernel<1, PD>.
+//
+// With CAND the tiles also keep, per batch row, the logits that can reach the
+// row's top-k pool, for the sampler's list mode.  The bound: every wave's
+// first tile is a fixed sample of the vocabulary (ns ids in all); a
+// workgroup's per-row maximum over its four first tiles goes by atomicMax into
+// slot blockIdx % 64 of the row, and a wave's bound is the ks-th largest slot,
+// ks = ceil(lam + 6 sqrt(lam) + 6) with lam = k ns / V.  It exceeds the row's
+// k-th largest only when ks of the row's top-k fall in the sample (each such
+// value raises at most one slot), which for a random placement of the top-k
+// is a Poisson tail of negligible mass.  Slots still empty when a wave reads
+// them only lower its bound, and the final slots give a bound at least every
+// wave's, so the sampler recomputes it from them and checks it (at least k
+// list values at or above it), streaming the row otherwise.  A wave reads the
+// slots after its second tile (or its only one) and filters its first tile's
+// values then.  Passing values are staged per workgroup in LDS (CAND_ROW per
+// row) and written out at its end, one atomic per row reserving their place
+// in the row's list.  A nan logit or a full stage or list flags the row.
+constexpr int CAND_ROW = 32;
 constexpr int LMX_MAXN = 4096;
+struct HeadCand {
+    int4 *hmeta;      // [row * HMETA_STRIDE] (count, -, -, flags: 1 full, 2 nan)
+    unsigned *hslots; // [row][64]
+    float *lval;      // [row][hcap]
+    int *lidx;
+    int hcap;
+    int ks;           // 1..64
+};
+
+// Per-workgroup candidate stage of lm_head_packed_xres_kernel<true>.
+struct CandStage {
+    unsigned wgmax[16];  // per-row maximum key of the workgroup's first tiles
+    int done0;           // waves past their first tile
+    int cnt[16];         // staged values per row (may exceed CAND_ROW: full)
+    int base[16];        // the row list positions reserved at the end
+    float val[16 * CAND_ROW];
+    int id[16 * CAND_ROW];
+};
+
+// stage this lane's value y of row `row` (vocab v) when it passes
+__device__ __forceinline__ void cand_stage(CandStage &CS, int row, float y, int v, bool pass)
+{
+    if (!__ballot(pass)) return;
+    if (pass) {
+        const int pos = atomicAdd(&CS.cnt[row], 1);
+        if (pos < CAND_ROW) {
+            CS.val[row * CAND_ROW + pos] = y;
+            CS.id[row * CAND_ROW + pos] = v;
+        }
+    }
+}
+
+template <bool CAND>
 __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(const int8_t *xq, const float *sx, int n,
                                                                              const int8_t *wpk, const float *sw,
                                                                              int V, float *logits, int ld, int b0,
-                                                                             int nb)
+                                                                             int nb, HeadCand C)
 {
     __shared__ __align__(16) int8_t xs[16 * LMX_MAXN];
     __shared__ __align__(16) float ot[LMM_WAVES][16 * 16];  // a finished tile, row-major
+    __shared__ CandStage CS;
     const int wv = wave_id(), lane = lane_id(), tid = threadIdx.x;
     const int g = lane >> 4, r16 = lane & 15;
+    if (CAND) {
+        if (tid < 16) {
+            CS.wgmax[tid] = 0u;
+            CS.cnt[tid] = 0;
+        }
+        if (tid == 0) CS.done0 = 0;
+    }
     const int npass = (n + LMM_KC - 1) / LMM_KC;
     const int nc64 = (n + 63) / 64;  // 1 KB blocks per 16-row tile
     const int ntile = (V + 15) / 16;
@@ -3077,15 +3338,21 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     const int nround = (thi - tlo + LMM_WAVES - 1) / LMM_WAVES;
     const int nstep = nround * npass;
 
-    // w of (round r, pass p): this wave's tile, blocks 4p .. 4p+3
+    // w of (round r, pass p): this wave's tile, blocks 4p .. 4p+3.  Every
+    // load is issued (a wave past its tiles reads its workgroup's first tile,
+    // blocks past the row read its last one): with no branch around them the
+    // compiler counts the loads in flight exactly and waits only for the step
+    // it multiplies.  The extra products are exact zeros (the activations of
+    // blocks past n are zero in LDS) or belong to tiles that are not stored.
     auto fetch_w = [&](v4i (&f)[4], int r, int p) {
         const int T = tlo + r * LMM_WAVES + wv;
         const bool ok = r < nround && T < thi;
-        const v4i *base = reinterpret_cast<const v4i *>(wpk + ((size_t)(ok ? T : 0) * nc64) * 1024) + lane;
+        const int Tc = min(ok ? T : tlo, ntile - 1);
+        const v4i *base = reinterpret_cast<const v4i *>(wpk + ((size_t)Tc * nc64) * 1024) + lane;
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
-            const int c = 4 * p + s4;
-            f[s4] = (ok && c < nc64) ? __builtin_nontemporal_load(base + (size_t)c * 64) : v4i{0, 0, 0, 0};
+            const int c = min(4 * p + s4, nc64 - 1);
+            f[s4] = __builtin_nontemporal_load(base + (size_t)c * 64);
         }
     };
     // the activations (chunk c = (row, c16), 16 bytes at k = 16 c16 of row
@@ -3123,6 +3390,9 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
             *reinterpret_cast<v4i *>(&xs[(kb * 64 + slot) * 16]) = xr[j];
         }
     }
+    // blocks of the last pass past the row: zero activations
+    for (int i = tid; i < (4 * npass - nc64) * 64; i += 64 * LMM_WAVES)
+        *reinterpret_cast<v4i *>(&xs[(nc64 * 64 + i) * 16]) = v4i{0, 0, 0, 0};
     __syncthreads();
     if (nstep == 0) return;
 
@@ -3131,11 +3401,102 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
 #pragma unroll
     for (int i = 0; i < 4; ++i) sxr[i] = (4 * g + i < nb) ? sx[b0 + 4 * g + i] : 0.0f;
     const bool vec_out = ((ld & 3) == 0) && ((((uintptr_t)logits) & 15) == 0);
+    // candidate state: the first tile's values, this lane's rows' bounds
+    float y0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, bnd[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
+    bool ok0[4] = {false, false, false, false};
+    int v0 = 0;
+    bool have_bnd = false;
+    auto take_bound = [&]() __attribute__((always_inline)) {
+        // the ks-th largest slot of every row, 16 rows side by side (bit by
+        // bit, ballot counts), then the first tile's values against it
+        uint32_t sk[16], K[16];
+#pragma unroll
+        for (int bb = 0; bb < 16; ++bb) {
+            sk[bb] = (bb < nb) ? __hip_atomic_load(&C.hslots[(size_t)(b0 + bb) * 64 + lane], __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT)
+                               : 0u;
+            K[bb] = 0u;
+        }
+#pragma unroll 1
+        for (int bit = 31; bit >= 0; --bit) {
+#pragma unroll
+            for (int bb = 0; bb < 16; ++bb) {
+                const uint32_t cand = K[bb] | (1u << bit);
+                if (__popcll(__ballot(sk[bb] >= cand)) >= C.ks) K[bb] = cand;
+            }
+        }
+#pragma unroll
+        for (int bb = 0; bb < 16; ++bb) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (4 * g + i == bb) bnd[i] = K[bb] ? keyf(K[bb]) : -INFINITY;
+        }
+        have_bnd = true;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) cand_stage(CS, 4 * g + i, y0[i], v0, ok0[i] && y0[i] >= bnd[i]);
+    };
+    v4i acc_c = {0, 0, 0, 0};  // a finished tile waiting for cand_tile
+    float sw_c = 0.0f;
+    int t_c = 0, r_c = 0;
+    bool pend = false;
+    auto cand_tile = [&]() __attribute__((always_inline)) {
+        const int v = 16 * t_c + r16;
+        const float swv = (v < V) ? sw_c : 0.0f;
+        float y[4];
+        bool ok[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            ok[i] = v < V && 4 * g + i < nb;
+            y[i] = (sxr[i] * swv) * (float)acc_c[i];
+        }
+        if (__ballot((ok[0] && y[0] != y[0]) || (ok[1] && y[1] != y[1]) || (ok[2] && y[2] != y[2]) ||
+                     (ok[3] && y[3] != y[3]))) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+                if (ok[i] && y[i] != y[i]) atomicOr(&C.hmeta[(size_t)(b0 + 4 * g + i) * HMETA_STRIDE].w, 2);
+        }
+        if (r_c == 0) {
+            // the sample: per-row maxima of the 16 lanes of a group, then of
+            // the workgroup's waves in LDS; the last wave past its first tile
+            // publishes them to the row's slot (one atomic per row)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                uint32_t m = ok[i] ? fkey(y[i]) : 0u;
+                m = max(m, (uint32_t)__shfl_xor((int)m, 1, 64));
+                m = max(m, (uint32_t)__shfl_xor((int)m, 2, 64));
+                m = max(m, (uint32_t)__shfl_xor((int)m, 4, 64));
+                m = max(m, (uint32_t)__shfl_xor((int)m, 8, 64));
+                if (r16 == 0 && 4 * g + i < nb && m) atomicMax(&CS.wgmax[4 * g + i], m);
+                y0[i] = y[i];
+                ok0[i] = ok[i];
+            }
+            v0 = v;
+            int prev = 0;
+            if (lane == 0) prev = atomicAdd(&CS.done0, 1);
+            prev = __builtin_amdgcn_readfirstlane(prev);
+            if (prev == min(LMM_WAVES, thi - tlo) - 1 && lane < nb) {
+                const unsigned m = CS.wgmax[lane];
+                if (m) atomicMax(&C.hslots[(size_t)(b0 + lane) * 64 + (blockIdx.x & 63)], m);
+            }
+        } else {
+            if (!have_bnd) take_bound();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) cand_stage(CS, 4 * g + i, y[i], v, ok[i] && y[i] >= bnd[i]);
+        }
+        pend = false;
+    };
     v4i acc = {0, 0, 0, 0};
     int r = 0, p = 0;  // position of step s
-    auto step = [&](v4i (&wc)[4], v4i (&wn)[4]) {
+    // sw of this lane's vocab row in the current tile, loaded one step ahead
+    // (unconditionally, like W)
+    auto sw_of = [&](int rr) {
+        return sw[min(16 * min(tlo + rr * LMM_WAVES + wv, ntile - 1) + r16, V - 1)];
+    };
+    float sw_cur = sw_of(0);
+    auto step = [&](v4i (&wc)[4], v4i (&wn)[4]) __attribute__((always_inline)) {
         fetch_w(wn, rw, pw);  // step s + 3
         advance();
+        const float sw_next = sw_of(r + (p + 1 == npass ? 1 : 0));
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
             const int slot = g * 16 + ((r16 + g + 4 * s4) & 15);
@@ -3147,7 +3508,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
             if (T < thi && nb <= 4) {
                 const int v = 16 * T + r16;
                 if (v < V) {
-                    const float swv = sw[v];
+                    const float swv = sw_cur;
 #pragma unroll
                     for (int i = 0; i < 4; ++i) {
                         const int bb = 4 * g + i;
@@ -3161,7 +3522,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
                 // instead of four scattered ones (the store count, not the
                 // bytes, costs at 5-16 rows)
                 const int v = 16 * T + r16;
-                const float swv = (v < V) ? sw[v] : 0.0f;
+                const float swv = (v < V) ? sw_cur : 0.0f;
                 float *o = ot[wv];
 #pragma unroll
                 for (int i = 0; i < 4; ++i) o[(4 * g + i) * 16 + r16] = (sxr[i] * swv) * (float)acc[i];
@@ -3180,16 +3541,51 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
                 }
                 wave_sync();  // the tile buffer is read before the next tile writes it
             }
+            if (CAND && T < thi) {
+                // handled after this group of four steps (a tile spans at
+                // least four, so at most one is pending)
+                acc_c = acc;
+                sw_c = sw_cur;
+                t_c = T;
+                r_c = r;
+                pend = true;
+            }
             acc = v4i{0, 0, 0, 0};
             p = 0;
             ++r;
         }
+        sw_cur = sw_next;
     };
     for (int s = 0; s < nstep; s += 4) {
         step(w0, w3);
         if (s + 1 < nstep) step(w1, w0);
         if (s + 2 < nstep) step(w2, w1);
         if (s + 3 < nstep) step(w3, w2);
+        if (CAND && pend) cand_tile();
+    }
+    // a wave with one tile reads the slots at its end
+    if (CAND && !have_bnd && tlo + wv < thi) take_bound();
+    if (CAND) {
+        // the staged values go to their rows' lists
+        __syncthreads();
+        if (tid < nb) {
+            const int c = CS.cnt[tid];
+            const int put = min(c, CAND_ROW);
+            int base = 0;
+            int4 *hm = C.hmeta + (size_t)(b0 + tid) * HMETA_STRIDE;
+            if (put > 0) base = atomicAdd(&hm->x, put);
+            CS.base[tid] = base;
+            if (c > CAND_ROW || base + put > C.hcap) atomicOr(&hm->w, 1);
+        }
+        __syncthreads();
+        for (int e = tid; e < nb * CAND_ROW; e += 64 * LMM_WAVES) {
+            const int row = e / CAND_ROW, j = e - row * CAND_ROW;
+            const int pos = CS.base[row] + j;
+            if (j < min(CS.cnt[row], CAND_ROW) && pos < C.hcap) {
+                C.lval[(size_t)(b0 + row) * C.hcap + pos] = CS.val[e];
+                C.lidx[(size_t)(b0 + row) * C.hcap + pos] = CS.id[e];
+            }
+        }
     }
 }
 
@@ -3693,6 +4089,54 @@ __global__ void expf_check_kernel(uint32_t first_hi, int nhi, uint64_t *out)
     (void)nhi;
 }
 
+// Pre-pass of a call with a bias: the nonzero map and the maximum the
+// sampler's stream filter bounds bias[e] with.  Bit e of bits is set unless
+// bias[e] is +0.0 (x + +0.0 is what the filter computes for a clear bit, so
+// its value is exact there; -0.0 is flagged, since x + -0.0 differs from
+// x + +0.0 at x = -0.0).  part[block] is the largest order key over the
+// block's flagged entries, all ones when one of them is a nan or -inf (their
+// sums can be nans the bound would miss; the bound is then a nan and the
+// rows take the nan path), 0 when none is flagged.  Blocks cover per_blk
+// elements each (a multiple of 1024); each thread 4 consecutive elements per
+// step, the 8 lanes of a word merged by shuffles.
+__global__ __launch_bounds__(WG) void bias_prep_kernel(const float *bias, int V, int per_blk, uint32_t *bits,
+                                                       uint32_t *part)
+{
+    __shared__ uint32_t red[NWAVE];
+    const int lane = lane_id();
+    const int beg = blockIdx.x * per_blk;
+    const int end = min(V, beg + per_blk);
+    uint32_t kmax = 0u;
+    for (int base = beg; base < end; base += 4 * WG) {
+        const int e0 = base + 4 * (int)threadIdx.x;
+        uint32_t nib = 0u;
+#pragma unroll
+        for (int c = 0; c < 4; ++c) {
+            if (e0 + c < end) {
+                const float v = bias[e0 + c];
+                if (__float_as_uint(v) != 0u) {
+                    nib |= 1u << c;
+                    kmax = max(kmax, (v != v || v == -INFINITY) ? 0xFFFFFFFFu : fkey(v));
+                }
+            }
+        }
+        uint32_t word = nib << (4 * (lane & 7));
+        word |= (uint32_t)__shfl_xor((int)word, 1, 64);
+        word |= (uint32_t)__shfl_xor((int)word, 2, 64);
+        word |= (uint32_t)__shfl_xor((int)word, 4, 64);
+        if ((lane & 7) == 0 && e0 < V) bits[e0 >> 5] = word;
+    }
+    kmax = wave_max_u(kmax);
+    if (lane == 0) red[wave_id()] = kmax;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        uint32_t m = red[0];
+#pragma unroll
+        for (int w = 1; w < NWAVE; ++w) m = max(m, red[w]);
+        part[blockIdx.x] = m;
+    }
+}
+
 }  // namespace
 
 // ===========================================================================
@@ -3708,6 +4152,7 @@ struct lal_gpu_ctx {
     int lmh_wg;         // LAL_GPU_LMH_WG: workgroups per CU
     int lmh_xres;       // LAL_GPU_LMH_XRES: 0 disables the resident-activation kernel
     int lmh_pd;         // LAL_GPU_LMH_PD: W steps in flight (2 or 3)
+    int list_ks;        // LAL_GPU_LIST_KS: rank of lal_gpu_lm_head_sample's bound (0: from k)
     // slice lists (see KArgs): max_batch x FLAT_MAX entries, metadata for up
     // to MAX_SLICES slices per row, one arrival counter per row (zeroed here,
     // reset by every row's finisher)
@@ -3716,6 +4161,13 @@ struct lal_gpu_ctx {
     int4 *lst_meta;
     unsigned *arrive;
     int *rr_ids;  // [max_batch][RERANK_MAX] ids kept by lal_gpu_lm_head_rerank's selection
+    uint32_t *bias_bits;  // [ceil(max_vocab / 32)] nonzero map of a call's bias
+    uint32_t *bias_part;  // [WG] its per-block maximum keys
+    // lal_gpu_lm_head_sample's candidate state (zeroed here, cleared again by
+    // the sampler after each use): per row (count, -, -, flags) every
+    // HMETA_STRIDE int4 and 64 sample slots; the lists are lst_val / lst_idx
+    int4 *hmeta;
+    unsigned *hslots;
 };
 
 static thread_local hipError_t g_last_hip = hipSuccess;
@@ -3787,6 +4239,7 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     if (const char *env = getenv("LAL_GPU_LMH_WG")) c->lmh_wg = std::max(0, atoi(env));
     if (const char *env = getenv("LAL_GPU_LMH_XRES")) c->lmh_xres = atoi(env) != 0;
     if (const char *env = getenv("LAL_GPU_LMH_PD")) c->lmh_pd = (atoi(env) == 3) ? 3 : 2;
+    if (const char *env = getenv("LAL_GPU_LIST_KS")) c->list_ks = std::min(64, std::max(0, atoi(env)));
     const size_t nl = (size_t)max_batch * FLAT_MAX;
     hipError_t e = hipMalloc((void **)&c->lst_val, nl * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->lst_idx, nl * sizeof(int));
@@ -3794,6 +4247,12 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     if (e == hipSuccess) e = hipMalloc((void **)&c->arrive, (size_t)max_batch * sizeof(unsigned));
     if (e == hipSuccess) e = hipMemset(c->arrive, 0, (size_t)max_batch * sizeof(unsigned));
     if (e == hipSuccess) e = hipMalloc((void **)&c->rr_ids, (size_t)max_batch * RERANK_MAX * sizeof(int));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->bias_bits, (size_t)((max_vocab + 31) / 32) * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->bias_part, (size_t)WG * sizeof(uint32_t));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->hmeta, (size_t)max_batch * HMETA_STRIDE * sizeof(int4));
+    if (e == hipSuccess) e = hipMemset(c->hmeta, 0, (size_t)max_batch * HMETA_STRIDE * sizeof(int4));
+    if (e == hipSuccess) e = hipMalloc((void **)&c->hslots, (size_t)max_batch * 64 * sizeof(unsigned));
+    if (e == hipSuccess) e = hipMemset(c->hslots, 0, (size_t)max_batch * 64 * sizeof(unsigned));
     if (e != hipSuccess) {
         lal_gpu_destroy(c);
         return e == hipErrorOutOfMemory ? LAL_GPU_E_NOMEM : hip_fail(e);
@@ -3812,6 +4271,10 @@ void lal_gpu_destroy(lal_gpu_ctx *ctx)
     if (ctx->lst_meta) (void)hipFree(ctx->lst_meta);
     if (ctx->arrive) (void)hipFree(ctx->arrive);
     if (ctx->rr_ids) (void)hipFree(ctx->rr_ids);
+    if (ctx->bias_bits) (void)hipFree(ctx->bias_bits);
+    if (ctx->bias_part) (void)hipFree(ctx->bias_part);
+    if (ctx->hmeta) (void)hipFree(ctx->hmeta);
+    if (ctx->hslots) (void)hipFree(ctx->hslots);
     if (cur >= 0 && cur != ctx->device) (void)hipSetDevice(cur);
     free(ctx);
 }
@@ -3844,6 +4307,14 @@ struct ListTarget {
     int *lst_idx;
     int4 *lst_meta;
     unsigned *arrive;
+    uint32_t *bias_bits;  // nonzero map of the bias for up to bias_vocab ids
+    uint32_t *bias_part;  // [WG]
+    int bias_vocab;
+    // list mode (an LM head's candidate lists in lst_val / lst_idx)
+    bool list = false;
+    int4 *hmeta = nullptr;
+    unsigned *hslots = nullptr;
+    int hks = 0;
 };
 
 static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gpu_sample_params *p,
@@ -3933,6 +4404,14 @@ static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gp
     const int flat = NWAVE * (small ? CAPW_SMALL : CAPW_LARGE);
     A.batch = batch;
     A.nslice = (batch <= t.slice_rows) ? choose_slices(batch, vocab, k_eff, flat, t.forced_slices) : 1;
+    if (t.list) {
+        if (A.bias || A.allow) return LAL_GPU_E_INVAL;
+        A.nslice = 1;
+        A.hmeta = t.hmeta;
+        A.hslots = t.hslots;
+        A.hcap = FLAT_MAX;
+        A.hks = t.hks;
+    }
     A.ncu = t.ncu;
     A.lcap = flat / A.nslice;
     // a slice list must hold more than k values (see the finisher): always
@@ -3943,6 +4422,17 @@ static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gp
     A.lst_idx = t.lst_idx;
     A.lst_meta = t.lst_meta;
     A.arrive = t.arrive;
+    if (A.bias) {
+        // the bias's nonzero map and maxima, ahead of the sampler in the stream
+        if (vocab > t.bias_vocab) return LAL_GPU_E_RANGE;
+        const int per_blk = std::max(4 * WG, (int)((((long long)vocab + WG - 1) / WG + 4 * WG - 1) /
+                                                  (4 * WG) * (4 * WG)));
+        A.bias_nparts = (vocab + per_blk - 1) / per_blk;
+        A.bias_bits = t.bias_bits;
+        A.bias_part = t.bias_part;
+        hipLaunchKernelGGL(bias_prep_kernel, dim3((unsigned)A.bias_nparts), dim3(WG), 0, s, A.bias, vocab, per_blk,
+                           t.bias_bits, t.bias_part);
+    }
     const dim3 grid((unsigned)(((batch + 7) / 8) * 8 * A.nslice)), block(WG);
 #define LAL_LAUNCH(HB, HA)                                                                   \
     do {                                                                                     \
@@ -3951,7 +4441,12 @@ static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gp
         else                                                                                 \
             hipLaunchKernelGGL((sample_rows_kernel<HB, HA, CAPW_LARGE>), grid, block, 0, s, A); \
     } while (0)
-    if (A.bias && A.allow) LAL_LAUNCH(true, true);
+    if (t.list) {
+        if (small)
+            hipLaunchKernelGGL((sample_rows_kernel<false, false, CAPW_SMALL, true>), grid, block, 0, s, A);
+        else
+            hipLaunchKernelGGL((sample_rows_kernel<false, false, CAPW_LARGE, true>), grid, block, 0, s, A);
+    } else if (A.bias && A.allow) LAL_LAUNCH(true, true);
     else if (A.bias) LAL_LAUNCH(true, false);
     else if (A.allow) LAL_LAUNCH(false, true);
     else LAL_LAUNCH(false, false);
@@ -3971,6 +4466,8 @@ struct NoallocScratch {
     int lst_idx[LAL_GPU_NOALLOC_MAX_ROWS * FLAT_MAX];
     int4 lst_meta[LAL_GPU_NOALLOC_MAX_ROWS * MAX_SLICES];
     unsigned arrive[LAL_GPU_NOALLOC_MAX_ROWS];
+    uint32_t bias_bits[LAL_GPU_NOALLOC_MAX_BIAS_VOCAB / 32];
+    uint32_t bias_part[WG];
 };
 static __device__ __align__(256) NoallocScratch scratch;
 
@@ -4033,6 +4530,9 @@ int lal_gpu_sample_noalloc(int batch, int vocab, const lal_gpu_sample_params *pa
     t.lst_idx = d.ptr->lst_idx;
     t.lst_meta = d.ptr->lst_meta;
     t.arrive = d.ptr->arrive;
+    t.bias_bits = d.ptr->bias_bits;
+    t.bias_part = d.ptr->bias_part;
+    t.bias_vocab = LAL_GPU_NOALLOC_MAX_BIAS_VOCAB;
     return launch_sample(t, batch, vocab, params, io, stream);
 }
 
@@ -4049,6 +4549,9 @@ int lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab, const lal_gpu_sample_
     t.lst_idx = ctx->lst_idx;
     t.lst_meta = ctx->lst_meta;
     t.arrive = ctx->arrive;
+    t.bias_bits = ctx->bias_bits;
+    t.bias_part = ctx->bias_part;
+    t.bias_vocab = ctx->max_vocab;
     return launch_sample(t, batch, vocab, p, io, stream);
 }
 
@@ -4199,8 +4702,8 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
         const unsigned nwg = (unsigned)std::max(1, std::min(per_cu * ctx->ncu, (ntile + LMM_WAVES - 1) / LMM_WAVES));
         const dim3 g2(nwg), blk(64 * LMM_WAVES);
         if (xres) {
-            hipLaunchKernelGGL(lm_head_packed_xres_kernel, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits,
-                               ld, b0, nb);
+            hipLaunchKernelGGL(lm_head_packed_xres_kernel<false>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab,
+                               d_logits, ld, b0, nb, HeadCand{});
             LAL_HIP(hipGetLastError());
             continue;
         }
@@ -4222,6 +4725,67 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
         LAL_HIP(hipGetLastError());
     }
     return LAL_GPU_OK;
+}
+
+int lal_gpu_lm_head_sample(lal_gpu_ctx *ctx, const float *d_x, int batch, int n, int8_t *d_xq, float *d_sx,
+                           const int8_t *d_wpk, const float *d_sw, int vocab, float *d_logits, int ld,
+                           const lal_gpu_sample_params *p, const lal_gpu_sample_io *io, void *stream)
+{
+    if (!ctx || !d_x || !d_xq || !d_sx || !d_wpk || !d_sw || !d_logits || !p || !io) return LAL_GPU_E_INVAL;
+    if (batch <= 0 || n <= 0 || vocab <= 0 || ld < vocab) return LAL_GPU_E_INVAL;
+    if (batch > ctx->max_batch || vocab > ctx->max_vocab) return LAL_GPU_E_RANGE;
+    if (((uintptr_t)d_xq & 15) || ((uintptr_t)d_wpk & 15) || (n & 15)) return LAL_GPU_E_INVAL;
+    lal_gpu_sample_io sio = *io;
+    sio.logits = d_logits;
+    sio.ld = ld;
+    int rc = lal_gpu_quantize_x(ctx, d_x, batch, n, 0, d_xq, d_sx, stream);
+    if (rc != LAL_GPU_OK) return rc;
+    // candidate lists from the head: up to 16 rows (activations resident),
+    // no bias or allow mask (the list holds raw logits), and a sample bound
+    // (ks <= 64 slots) for the row's k
+    const bool greedy = !(p->temperature > 0.0f) || p->top_k <= 0;
+    const int k_eff = greedy ? 1 : std::min(std::max(p->top_k, 1), vocab);
+    const int ntile = (vocab + 15) / 16;
+    const unsigned nwg = (unsigned)std::max(1, std::min((ctx->lmh_wg > 0 ? ctx->lmh_wg : 2) * ctx->ncu,
+                                                        (ntile + LMM_WAVES - 1) / LMM_WAVES));
+    const double ns = std::min((double)vocab, 16.0 * std::min((double)ntile, (double)nwg * LMM_WAVES));
+    const double lam = (double)k_eff * ns / (double)vocab;
+    const int ks = ctx->list_ks > 0 ? ctx->list_ks : (int)std::ceil(lam + 6.0 * std::sqrt(lam) + 6.0);
+    // (a tile spans at least four 256-byte passes of k: at most one finished
+    // tile per group of four steps waits for the candidate code)
+    const bool cand = batch <= 16 && n <= LMX_MAXN && n > 3 * LMM_KC && ctx->lmh_xres != 0 && !io->allow_bits &&
+                      !io->bias && ks <= 64 && k_eff <= LAL_GPU_MAX_K;
+    if (!cand) {
+        rc = lal_gpu_lm_head_q8_packed(ctx, d_xq, d_sx, batch, n, d_wpk, d_sw, vocab, d_logits, ld, stream);
+        if (rc != LAL_GPU_OK) return rc;
+        return lal_gpu_sample(ctx, batch, vocab, p, &sio, stream);
+    }
+    HeadCand C;
+    C.hmeta = ctx->hmeta;
+    C.hslots = ctx->hslots;
+    C.lval = ctx->lst_val;
+    C.lidx = ctx->lst_idx;
+    C.hcap = FLAT_MAX;
+    C.ks = ks;
+    hipLaunchKernelGGL(lm_head_packed_xres_kernel<true>, dim3(nwg), dim3(64 * LMM_WAVES), 0, (hipStream_t)stream,
+                       d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, 0, batch, C);
+    LAL_HIP(hipGetLastError());
+    ListTarget t;
+    t.ncu = ctx->ncu;
+    t.forced_slices = 1;
+    t.slice_rows = ctx->max_batch;
+    t.lst_val = ctx->lst_val;
+    t.lst_idx = ctx->lst_idx;
+    t.lst_meta = ctx->lst_meta;
+    t.arrive = ctx->arrive;
+    t.bias_bits = ctx->bias_bits;
+    t.bias_part = ctx->bias_part;
+    t.bias_vocab = ctx->max_vocab;
+    t.list = true;
+    t.hmeta = ctx->hmeta;
+    t.hslots = ctx->hslots;
+    t.hks = ks;
+    return launch_sample(t, batch, vocab, p, &sio, stream);
 }
 
 int lal_gpu_lm_head_rerank(lal_gpu_ctx *ctx, const float *d_x, int batch, int n, const int8_t *d_wq,

@@ -8,6 +8,7 @@
  */
 #include "lal_oracle.h"
 
+#include <limits.h>
 #include <math.h>
 #include <stdlib.h>
 #include <string.h>
@@ -374,20 +375,55 @@ void lal_oracle_uniforms(unsigned seed, int n, float *out, int gpt2)
 /* lal_q8_kernel.h:375-442.  The AVX2 build converts the multiple-of-8 prefix
  * with round-to-nearest-even (cvtps_epi32 under the default MXCSR) and the
  * remainder with C truncation; the scalar build truncates everything. */
+/* x86 float -> int32 conversions as the reference's builds execute them
+ * (cvtps2dq rounds to nearest even; cvttss2si, C's (int) cast, truncates):
+ * a nan or a value outside the int32 range gives INT_MIN ("integer
+ * indefinite"). */
+static int x86_cvt(float v, int round_even)
+{
+    if (!(v >= -2147483648.0f && v < 2147483648.0f)) return INT_MIN;
+    return round_even ? (int)nearbyintf(v) : (int)v;
+}
+
+/* _mm_max_ps / _mm256_max_ps: the first operand if it is greater, else the
+ * second (so a nan in either operand gives the second). */
+static float x86_maxps(float a, float b)
+{
+    return (a > b) ? a : b;
+}
+
+/* lal_q8_kernel.h:375-445 (lal_quantize_x_int8).  mode 0, the AVX2 build
+ * (:376-428): |x| maxima in 8 lanes over the first n & ~7 values (lane j
+ * sees x[8c + j] in order, from 0), reduced as hi/lo halves then two shuffled
+ * steps (:387-392), the tail folded in with `a > max` (:393); values of the 8-
+ * aligned prefix rounded by cvtps2dq (:402-404), the tail truncated (:415);
+ * both clamped to [-127, 127].  mode 1, the scalar build (:429-443): `a > max`
+ * over all values, every value truncated and clamped. */
 float lal_oracle_quantize_x(const float *x, int8_t *xq, int n, int mode)
 {
     float m = 0.0f;
-    for (int i = 0; i < n; i++) {
+    int n8 = 0;
+    if (mode == 0) {
+        n8 = n & ~7;
+        float lane[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+        for (int i = 0; i < n8; i++) lane[i & 7] = x86_maxps(lane[i & 7], fabsf(x[i]));
+        float h[4];
+        for (int j = 0; j < 4; j++) h[j] = x86_maxps(lane[j], lane[j + 4]);
+        /* _MM_SHUFFLE(1,0,3,2): (h2, h3, h0, h1) */
+        const float s1[4] = {h[2], h[3], h[0], h[1]};
+        for (int j = 0; j < 4; j++) h[j] = x86_maxps(h[j], s1[j]);
+        /* _MM_SHUFFLE(0,0,0,1): element 0 takes h1 */
+        m = x86_maxps(h[0], h[1]);
+    }
+    for (int i = n8; i < n; i++) {
         float a = fabsf(x[i]);
         if (a > m) m = a;
     }
     float scale = m / 127.0f;
     if (scale < 1e-8f) scale = 1e-8f;
     float inv = 1.0f / scale;
-    int rne_end = (mode == 0) ? (n & ~7) : 0;
     for (int i = 0; i < n; i++) {
-        float s = x[i] * inv;
-        int q = (i < rne_end) ? (int)nearbyintf(s) : (int)s;
+        int q = x86_cvt(x[i] * inv, i < n8);
         if (q > 127) q = 127;
         if (q < -127) q = -127;
         xq[i] = (int8_t)q;

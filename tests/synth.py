@@ -198,5 +198,35 @@ def make_row(kind, seed, V):
     raise ValueError(kind)
 
 
+def quantize_special_rows():
+    """Activation rows with nans and infinities at the places the AVX2 build
+    treats differently: a lane's last 8-chunk (its nan survives the lane
+    maximum), earlier chunks (it does not), the scalar tail, and rows made of
+    them."""
+    rows = []
+    qnan, inf = np.float32(np.nan), np.float32(np.inf)
+    for n in (7, 8, 37, 256, 3584):
+        base = (normal(8100 + n, 0, n) * np.float32(3.0)).astype(np.float32)
+        n8 = n & ~7
+        places = {0, n // 2, n - 1}
+        if n8:
+            places |= {n8 - 1, n8 - 8, max(0, n8 - 9)}
+        for pos in sorted(places):
+            for val in (qnan, -qnan, inf, -inf):
+                x = base.copy()
+                x[pos] = val
+                rows.append(x)
+        x = base.copy()
+        x[::5] = qnan
+        rows.append(x)
+        rows.append(np.full(n, qnan, np.float32))
+        rows.append(np.full(n, inf, np.float32))
+        x = base.copy()
+        x[n // 3] = inf
+        x[n - 1] = qnan
+        rows.append(x)
+    return rows
+
+
 def _bits_f32(bits):
     return np.array([bits], np.uint32).view(np.float32)[0]

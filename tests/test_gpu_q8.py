@@ -103,6 +103,18 @@ def test_quantize_x_golden(dev):
             assert q[0].tobytes().hex() == rec[sfx]["xq"]
 
 
+def test_quantize_x_nan_inf(dev, orc):
+    """Rows with nans and infinities where the AVX2 build's lane maximum and
+    x86 conversions decide the result (the oracle is pinned to the compiled
+    reference on the same rows): scale bits and every value, both modes."""
+    for x in synth.quantize_special_rows():
+        for mode in (0, 1):
+            s, q = quantize(dev, x[None, :], mode)
+            so, qo = orc.quantize_x(x.copy(), mode)
+            assert s[0].view(np.uint32) == np.float32(so).view(np.uint32), (len(x), mode)
+            assert np.array_equal(q[0], qo), (len(x), mode, np.nonzero(q[0] != qo)[0][:8])
+
+
 def test_lm_head_golden(dev):
     for rec in golden_cases.load()["q8"]["lm_head"]:
         V, n, seed = rec["V"], rec["n"], rec["seed"]

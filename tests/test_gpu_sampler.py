@@ -149,6 +149,55 @@ def test_constrained_decoding(dev, run, orc):
         assert t not in set(hist[b].tolist())
 
 
+def bias_of_kind(kind, V):
+    """Shared biases for the stream filter's nonzero map: only +0.0 counts as
+    zero there, flagged entries are bounded by the largest one."""
+    b = synth.sparse_bias(41, V, max(1, V // 60), 3.0)
+    if kind == "signed_zero":  # -0.0 entries (flagged) and a few large ones
+        b[::5] = np.float32(-0.0)
+        b[7::997] = np.float32(9.0)
+    elif kind == "neg_inf":  # flagged -inf: the bound is a nan, rows take the nan path
+        b[3::1999] = np.float32(-np.inf)
+    elif kind == "pos_inf":
+        b[11::4001] = np.float32(np.inf)
+    elif kind == "nan":
+        b[V // 3] = np.float32(np.nan)
+    elif kind == "dense":  # every entry flagged
+        b = (synth.normal(43, 0, V) * np.float32(0.5)).astype(np.float32)
+    return b
+
+
+@pytest.mark.parametrize("nsl", [1, 3])
+@pytest.mark.parametrize("bkind", ["sparse", "signed_zero", "neg_inf", "pos_inf", "nan", "dense", "none"])
+def test_allow_and_bias_windows(orc, slices, bkind, nsl):
+    """Rows at every alignment (ld = V + 2, so the first aligned element moves
+    from row to row and a lane's 4 map bits can straddle two words), V not a
+    multiple of 32, allow masks and biases of every kind, with and without a
+    history, against the oracle."""
+    run = slices(nsl)
+    B, V = 8, 20011
+    ld = V + 2
+    kinds = ["gauss", "signed_zero", "ties", "neginf", "zipf", "outliers", "huge", "gauss"]
+    x = np.full((B, ld), np.nan, np.float32)
+    for b in range(B):
+        x[b, :V] = synth.make_row(kinds[b], 700 + b, V)
+    words = (V + 31) // 32
+    allow = synth.allow_bits(44, B, V, 0.3)
+    allow[3] = synth.allow_bits(45, 1, V, 0.002)[0]  # a nearly empty mask
+    bias = None if bkind == "none" else bias_of_kind(bkind, V)
+    u = np.array([0.0, 1.0, 0.5, 0.25, 0.999, 1e-7, 0.75, 0.3], np.float32)
+    hist = synth.history(46, B, 24, V)
+    for a, h, k, T in ((allow, hist, 40, 0.8), (None, hist, 1, 0.8), (allow, None, 300, 1.1),
+                       (None, None, 40, 0.7), (allow, hist, 7, 0.0)):
+        if a is None and bias is None:
+            continue
+        kw = dict(V=V, T=T, k=k, pen=1.2, hist=h, allow=a, bias=bias, u=u, cand_ld=320,
+                  mask_recent=3 if h is not None else 0)
+        log(f"windows bias {bkind} slices {nsl} allow {a is not None} hist {h is not None} k {k} T {T}")
+        assert_same(run(x, **kw), oracle_run(orc, x, **kw), cand_ld=320)
+    assert words == allow.shape[1]
+
+
 # ---------------------------------------------------------------------------
 # variants and edge cases
 # ---------------------------------------------------------------------------
@@ -261,14 +310,24 @@ def test_expf_matches_glibc_exhaustively(dev, orc):
 # ---------------------------------------------------------------------------
 @pytest.fixture
 def slices(monkeypatch):
-    def set_slices(n):
+    """slices(n) -> a runner on a context created with LAL_GPU_SLICES=n (the
+    variable is read when a context is created)."""
+    from lal_amd import abi
+    made = []
+
+    def with_slices(n):
         monkeypatch.setenv("LAL_GPU_SLICES", str(n))
-    yield set_slices
+        d = abi.Device(0, max_batch=1024, max_vocab=V7B)
+        made.append(d)
+        return GpuRun(d)
+    yield with_slices
+    for d in made:
+        d.close()
 
 
 @pytest.mark.parametrize("nsl", [2, 3, 7, 16])
-def test_sliced_rows_match_oracle(run, orc, slices, nsl):
-    slices(nsl)
+def test_sliced_rows_match_oracle(orc, slices, nsl):
+    run = slices(nsl)
     B, V = 8, 40009
     kinds = ["gauss", "ties", "zipf", "outliers", "neginf", "signed_zero", "ascending", "huge"]
     x = np.stack([synth.make_row(kinds[b], 900 + b, V) for b in range(B)])
@@ -283,9 +342,9 @@ def test_sliced_rows_match_oracle(run, orc, slices, nsl):
 
 
 @pytest.mark.parametrize("nsl", [2, 5])
-def test_sliced_qwen7b_batch(dev, run, orc, slices, nsl):
+def test_sliced_qwen7b_batch(dev, orc, slices, nsl):
     """The 1024 x 152064 top-k/top-p step with every row split."""
-    slices(nsl)
+    run = slices(nsl)
     B = 1024
     x = gpu_logits(dev, "zipf", B, V7B, V7B, 21)
     hist = synth.history(22, B, 256, V7B)
@@ -295,10 +354,10 @@ def test_sliced_qwen7b_batch(dev, run, orc, slices, nsl):
 
 
 @pytest.mark.parametrize("nsl", [1, 3])
-def test_pool_above_buffers_with_top_p(run, orc, slices, nsl):
+def test_pool_above_buffers_with_top_p(orc, slices, nsl):
     """Constant rows: the pool is the whole row (ties beyond every buffer), so
     the nucleus is formed by an id-order rescan of the row."""
-    slices(nsl)
+    run = slices(nsl)
     B, V = 4, 30011
     x = np.stack([synth.make_row("const", 5 + b, V) for b in range(B)])
     x[1, 100:200] += np.float32(0.5)   # a few larger values ahead of the tie group

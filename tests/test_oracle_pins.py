@@ -17,6 +17,8 @@ cover directly.
   pool) are checked against the reference's filtered sampler with the same
   plugin loaded.
 """
+import ctypes as C
+
 import numpy as np
 import pytest
 
@@ -375,3 +377,18 @@ def test_mini_greedy_filter_clears_id_zero():
         p.flags = 0
         tok, *_ = ORC.sample_row(row.copy(), p, u=0.5)
         assert tok == best
+
+
+@pytest.mark.parametrize("mode,sfx", [(0, "avx2"), (1, "scalar")])
+def test_quantize_x_nan_inf_matches_reference(ref, mode, sfx):
+    """lal_quantize_x_int8 (runtime/lal_q8_kernel.h:375-445) compiled from the
+    reference in both builds vs the oracle's restatement, on rows holding nans
+    and infinities: the scale's bits and every quantized value."""
+    f = getattr(ref.L, f"lal_ref_quantize_x_int8_{sfx}")
+    for x in synth.quantize_special_rows():
+        q_ref = np.zeros(len(x), np.int8)
+        s_ref = np.float32(f(x.ctypes.data_as(C.POINTER(C.c_float)), q_ref.ctypes.data_as(C.POINTER(C.c_int8)),
+                             len(x)))
+        s_orc, q_orc = ORC.quantize_x(x.copy(), mode)
+        assert np.array_equal(np.array([s_ref]).view(np.uint32), np.array([s_orc]).view(np.uint32)), (len(x),)
+        assert np.array_equal(q_ref, q_orc), (len(x), np.nonzero(q_ref != q_orc)[0][:8])
