@@ -2773,23 +2773,26 @@ __device__ __forceinline__ int x86_cvt(float v, bool round_even)
 // _mm_max_ps: the first operand if it is greater, else the second
 __device__ __forceinline__ float x86_maxps(float a, float b) { return (a > b) ? a : b; }
 
-__global__ __launch_bounds__(256) void quantize_x_kernel(const float *x, int n, int mode,
-                                                         int8_t *xq, float *sx)
+// Scale of one activation row as lal_quantize_x_int8 computes it, for one
+// 256-thread block (every thread calls it; barriers inside).  mode 0 (AVX2
+// build): lane j of the 8-wide maximum sees |x[8c + j]| in chunk order, and a
+// nan there is kept only while no later value of the lane follows, so thread
+// (segment s, lane j) folds its run of chunks into (nan seen, ends in nan,
+// maximum after its last nan) and lane j's 32 runs are folded in order; the
+// lanes then reduce as the build's shuffles do, and the tail is folded in with
+// `a > max`.  mode 1: `a > max` over all values, which never takes a nan.
+struct QxShared {
+    float seg_m[256];
+    int seg_f[256];
+    float red[4];
+};
+
+__device__ float qx_scale(const float *xr, int n, int mode, QxShared &Q)
 {
-    // mode 0 (AVX2 build): lane j of the 8-wide maximum sees |x[8c + j]| in
-    // chunk order; a nan there is kept only while no later value of the lane
-    // follows, so thread (segment s, lane j) folds its run of chunks into
-    // (nan seen, ends in nan, maximum after its last nan) and lane j's 32
-    // runs are folded in order.  mode 1: `a > max` over all values, which
-    // never takes a nan.
-    __shared__ float seg_m[256];
-    __shared__ int seg_f[256];
-    __shared__ float red[4];
-    const int b = blockIdx.x, t = threadIdx.x;
-    const float *xr = x + (size_t)b * n;
-    const int n8 = (mode == 0) ? (n & ~7) : 0;
+    const int t = threadIdx.x;
     float m = 0.0f;
     if (mode == 0) {
+        const int n8 = n & ~7;
         const int j = t & 7, sgi = t >> 3, nch = n8 >> 3;
         const int c0 = (int)(((long long)nch * sgi) / 32), c1 = (int)(((long long)nch * (sgi + 1)) / 32);
         float acc = -1.0f;  // -1: no value after the last nan
@@ -2804,29 +2807,30 @@ __global__ __launch_bounds__(256) void quantize_x_kernel(const float *x, int n, 
                 acc = fmaxf(acc, a);
             }
         }
-        seg_m[t] = acc;
-        seg_f[t] = f;
+        __syncthreads();  // Q is free (an earlier call's readers are done)
+        Q.seg_m[t] = acc;
+        Q.seg_f[t] = f;
         __syncthreads();
         if (t < 8) {
             float la = -1.0f;
             int lf = 0;
             for (int sg = 0; sg < 32; ++sg) {
-                const int ff = seg_f[sg * 8 + t];
+                const int ff = Q.seg_f[sg * 8 + t];
                 if (!(ff & 4)) continue;
                 if (ff & 1) {
                     lf = ff;
-                    la = seg_m[sg * 8 + t];
+                    la = Q.seg_m[sg * 8 + t];
                 } else {
                     lf = (lf & 1) | 4;
-                    la = fmaxf(la, seg_m[sg * 8 + t]);
+                    la = fmaxf(la, Q.seg_m[sg * 8 + t]);
                 }
             }
-            seg_m[t] = (lf & 2) ? __builtin_nanf("") : fmaxf(la, 0.0f);
+            Q.seg_m[t] = (lf & 2) ? __builtin_nanf("") : fmaxf(la, 0.0f);
         }
         __syncthreads();
         if (t == 0) {
             float h[4];
-            for (int q = 0; q < 4; ++q) h[q] = x86_maxps(seg_m[q], seg_m[q + 4]);
+            for (int q = 0; q < 4; ++q) h[q] = x86_maxps(Q.seg_m[q], Q.seg_m[q + 4]);
             const float s1[4] = {h[2], h[3], h[0], h[1]};
             for (int q = 0; q < 4; ++q) h[q] = x86_maxps(h[q], s1[q]);
             float mm = x86_maxps(h[0], h[1]);
@@ -2834,25 +2838,39 @@ __global__ __launch_bounds__(256) void quantize_x_kernel(const float *x, int n, 
                 const float a = fabsf(xr[i]);
                 if (a > mm) mm = a;
             }
-            red[0] = mm;
+            Q.red[0] = mm;
         }
         __syncthreads();
-        m = red[0];
+        m = Q.red[0];
     } else {
         for (int i = t; i < n; i += 256) m = fmaxf(m, fabsf(xr[i]));
         m = wave_max(m);
-        if (lane_id() == 0) red[wave_id()] = m;
         __syncthreads();
-        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+        if (lane_id() == 0) Q.red[wave_id()] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(Q.red[0], Q.red[1]), fmaxf(Q.red[2], Q.red[3]));
     }
     float scale = m / 127.0f;
     if (scale < 1e-8f) scale = 1e-8f;
+    return scale;
+}
+
+// q of x[i] (i < n8: rounded, else truncated), x86 conversion, clamped
+__device__ __forceinline__ int8_t qx_value(float x, float inv, bool round_even)
+{
+    return (int8_t)min(127, max(-127, x86_cvt(x * inv, round_even)));
+}
+
+__global__ __launch_bounds__(256) void quantize_x_kernel(const float *x, int n, int mode,
+                                                         int8_t *xq, float *sx)
+{
+    __shared__ QxShared Q;
+    const int b = blockIdx.x, t = threadIdx.x;
+    const float *xr = x + (size_t)b * n;
+    const float scale = qx_scale(xr, n, mode, Q);
     const float inv = 1.0f / scale;
-    for (int i = t; i < n; i += 256) {
-        int q = x86_cvt(xr[i] * inv, i < n8);
-        q = min(127, max(-127, q));
-        xq[(size_t)b * n + i] = (int8_t)q;
-    }
+    const int n8 = (mode == 0) ? (n & ~7) : 0;
+    for (int i = t; i < n; i += 256) xq[(size_t)b * n + i] = qx_value(xr[i], inv, i < n8);
     if (t == 0) sx[b] = scale;
 }
 
@@ -3275,10 +3293,11 @@ __global__ __launch_bounds__(256) void quantize_w_kernel(const float *w, int n, 
 // wave's, so the sampler recomputes it from them and checks it (at least k
 // list values at or above it), streaming the row otherwise.  A wave reads the
 // slots after its second tile (or its only one) and filters its first tile's
-// values then.  Passing values are staged per workgroup in LDS (CAND_ROW per
-// row) and written out at its end, one atomic per row reserving their place
-// in the row's list.  A nan logit or a full stage or list flags the row.
-constexpr int CAND_ROW = 32;
+// values then.  Passing values are staged per wave in LDS (CAND_ROW per row:
+// about 200 of a row's values pass over some 2000 waves) and written out by
+// the wave at its end, one atomic per row reserving their place in the row's
+// list.  A nan logit or a full stage or list flags the row.
+constexpr int CAND_ROW = 8;
 constexpr int LMX_MAXN = 4096;
 struct HeadCand {
     int4 *hmeta;      // [row * HMETA_STRIDE] (count, -, -, flags: 1 full, 2 nan)
@@ -3289,45 +3308,56 @@ struct HeadCand {
     int ks;           // 1..64
 };
 
-// Per-workgroup candidate stage of lm_head_packed_xres_kernel<true>.
+// Candidate stage of lm_head_packed_xres_kernel<true>: per wave, per row
+// CAND_ROW values, written out by the wave at its end.
 struct CandStage {
     unsigned wgmax[16];  // per-row maximum key of the workgroup's first tiles
     int done0;           // waves past their first tile
-    int cnt[16];         // staged values per row (may exceed CAND_ROW: full)
-    int base[16];        // the row list positions reserved at the end
-    float val[16 * CAND_ROW];
-    int id[16 * CAND_ROW];
+    int cnt[LMM_WAVES][16];  // staged values per row (may exceed CAND_ROW: full)
+    float val[LMM_WAVES][16 * CAND_ROW];
+    int id[LMM_WAVES][16 * CAND_ROW];
 };
 
 // stage this lane's value y of row `row` (vocab v) when it passes
-__device__ __forceinline__ void cand_stage(CandStage &CS, int row, float y, int v, bool pass)
+__device__ __forceinline__ void cand_stage(CandStage &CS, int wv, int row, float y, int v, bool pass)
 {
     if (!__ballot(pass)) return;
     if (pass) {
-        const int pos = atomicAdd(&CS.cnt[row], 1);
+        const int pos = atomicAdd(&CS.cnt[wv][row], 1);
         if (pos < CAND_ROW) {
-            CS.val[row * CAND_ROW + pos] = y;
-            CS.id[row * CAND_ROW + pos] = v;
+            CS.val[wv][row * CAND_ROW + pos] = y;
+            CS.id[wv][row * CAND_ROW + pos] = v;
         }
     }
 }
+
+// In-kernel activation quantization (lal_quantize_x_int8, AVX2 build) of up
+// to QX_ROWS rows: every workgroup quantizes the rows itself (they are small
+// and stay in L2) instead of waiting for a separate launch; workgroup 0
+// writes xq / sx out.
+constexpr int QX_ROWS = 4;
+struct HeadQuant {
+    const float *x;  // [nb][n] fp32 (16-byte aligned), or null: xq / sx are inputs
+    int8_t *xq;      // outputs of workgroup 0
+    float *sx;
+};
 
 template <bool CAND>
 __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(const int8_t *xq, const float *sx, int n,
                                                                              const int8_t *wpk, const float *sw,
                                                                              int V, float *logits, int ld, int b0,
-                                                                             int nb, HeadCand C)
+                                                                             int nb, HeadCand C, HeadQuant HQ)
 {
     __shared__ __align__(16) int8_t xs[16 * LMX_MAXN];
     __shared__ __align__(16) float ot[LMM_WAVES][16 * 16];  // a finished tile, row-major
     __shared__ CandStage CS;
+    __shared__ QxShared QS;
+    __shared__ float qsc[QX_ROWS][LMM_WAVES];  // per-row maxima, then scales
     const int wv = wave_id(), lane = lane_id(), tid = threadIdx.x;
     const int g = lane >> 4, r16 = lane & 15;
     if (CAND) {
-        if (tid < 16) {
-            CS.wgmax[tid] = 0u;
-            CS.cnt[tid] = 0;
-        }
+        if (tid < 16) CS.wgmax[tid] = 0u;
+        if (tid < 16 * LMM_WAVES) CS.cnt[tid >> 4][tid & 15] = 0;
         if (tid == 0) CS.done0 = 0;
     }
     const int npass = (n + LMM_KC - 1) / LMM_KC;
@@ -3361,14 +3391,68 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     constexpr int XR = 16 * (LMX_MAXN / 16) / (64 * LMM_WAVES);
     const int cpr = 4 * nc64;
     v4i xr[XR];
+    // in-kernel quantization: chunk j of this thread as fp32 (16 values)
+    constexpr int XQ = QX_ROWS * (LMX_MAXN / 16) / (64 * LMM_WAVES);
+    f32x4 xf[XQ][4];
+    if (CAND && HQ.x) {
 #pragma unroll
-    for (int j = 0; j < XR; ++j) {
-        const int c = tid + j * 64 * LMM_WAVES;
-        const int row = c / cpr, k = 16 * (c - row * cpr);
-        v4i v = {0, 0, 0, 0};
-        if (c < 16 * cpr && row < nb && k < n) v = *reinterpret_cast<const v4i *>(xq + (size_t)(b0 + row) * n + k);
-        xr[j] = v;
+        for (int j = 0; j < XQ; ++j) {
+            const int c = tid + j * 64 * LMM_WAVES;
+            const int row = c / cpr, k = 16 * (c - row * cpr);
+            const bool in = row < nb && k < n;
+            const f32x4 *src = reinterpret_cast<const f32x4 *>(HQ.x + (size_t)(b0 + (in ? row : 0)) * n + (in ? k : 0));
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xf[j][q] = in ? src[q] : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < XR; ++j) {
+            const int c = tid + j * 64 * LMM_WAVES;
+            const int row = c / cpr, k = 16 * (c - row * cpr);
+            v4i v = {0, 0, 0, 0};
+            if (c < 16 * cpr && row < nb && k < n)
+                v = *reinterpret_cast<const v4i *>(xq + (size_t)(b0 + row) * n + k);
+            xr[j] = v;
+        }
     }
+    float qscl[QX_ROWS];  // the row scales of the in-kernel quantization
+#pragma unroll
+    for (int r = 0; r < QX_ROWS; ++r) qscl[r] = 0.0f;
+    if (CAND && HQ.x) {
+        // per-row max |x| and whether the row holds a nan or an infinity
+        float m[QX_ROWS];
+        bool bad[QX_ROWS];
+#pragma unroll
+        for (int r = 0; r < QX_ROWS; ++r) {
+            m[r] = 0.0f;
+            bad[r] = false;
+        }
+#pragma unroll
+        for (int j = 0; j < XQ; ++j) {
+            const int row = (tid + j * 64 * LMM_WAVES) / cpr;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float a = fabsf(xf[j][q][e]);
+#pragma unroll
+                    for (int r = 0; r < QX_ROWS; ++r)
+                        if (row == r) {
+                            m[r] = fmaxf(m[r], a);
+                            bad[r] = bad[r] || !(a <= 3.402823466e38f);
+                        }
+                }
+        }
+#pragma unroll
+        for (int r = 0; r < QX_ROWS; ++r) {
+            const float mw = wave_max(m[r]);
+            const bool bw = __ballot(bad[r]) != 0ull;
+            if (lane_id() == 0) qsc[r][wv] = bw ? -1.0f : mw;
+        }
+    }
+    // W of the first three steps, after the activations' loads and maxima
+    // (loads complete in issue order: waiting for the activations does not
+    // wait for W)
     v4i w0[4], w1[4], w2[4], w3[4];
     int rw = 0, pw = 0;
     auto advance = [&]() {
@@ -3380,6 +3464,58 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     advance();
     fetch_w(w2, rw, pw);
     advance();
+    if (CAND && HQ.x) {
+        __syncthreads();
+        float *scl = qscl;
+#pragma unroll
+        for (int r = 0; r < QX_ROWS; ++r) {
+            float mm = 0.0f;
+            bool bb = false;
+#pragma unroll
+            for (int ww = 0; ww < LMM_WAVES; ++ww) {
+                bb = bb || qsc[r][ww] < 0.0f;
+                mm = fmaxf(mm, qsc[r][ww]);
+            }
+            if (r < nb && bb) {
+                // a nan or an infinity: the build's order decides the maximum
+                scl[r] = qx_scale(HQ.x + (size_t)(b0 + r) * n, n, 0, QS);
+            } else {
+                scl[r] = mm / 127.0f;
+                if (scl[r] < 1e-8f) scl[r] = 1e-8f;
+            }
+        }
+        if (blockIdx.x == 0 && tid < nb && tid < QX_ROWS) {
+#pragma unroll
+            for (int r = 0; r < QX_ROWS; ++r)
+                if (tid == r) HQ.sx[b0 + r] = scl[r];
+        }
+        // the quantized chunks (n is a multiple of 16: every value is in the
+        // rounded prefix)
+#pragma unroll
+        for (int j = 0; j < XQ; ++j) {
+            const int c = tid + j * 64 * LMM_WAVES;
+            const int row = c / cpr, k = 16 * (c - row * cpr);
+            float sc = 1.0f;
+#pragma unroll
+            for (int r = 0; r < QX_ROWS; ++r)
+                if (row == r) sc = scl[r];
+            const float inv = 1.0f / sc;
+            int w4[4];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                uint32_t u = 0;
+#pragma unroll
+                for (int e = 0; e < 4; ++e) u |= (uint32_t)(uint8_t)qx_value(xf[j][q][e], inv, true) << (8 * e);
+                w4[q] = (int)u;
+            }
+            const v4i v = {w4[0], w4[1], w4[2], w4[3]};
+            const bool in = row < nb && k < n;
+            xr[j] = in ? v : v4i{0, 0, 0, 0};
+            if (blockIdx.x == 0 && in) *reinterpret_cast<v4i *>(HQ.xq + (size_t)(b0 + row) * n + k) = v;
+        }
+#pragma unroll
+        for (int j = XQ; j < XR; ++j) xr[j] = v4i{0, 0, 0, 0};
+    }
 #pragma unroll
     for (int j = 0; j < XR; ++j) {
         const int c = tid + j * 64 * LMM_WAVES;
@@ -3398,8 +3534,15 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
 
     // the scales of this lane's 4 batch rows, loaded once
     float sxr[4];
+    if (CAND && HQ.x) {
+        // the row scales as this workgroup computed them (rows < QX_ROWS:
+        // only lanes of group 0 have rows)
 #pragma unroll
-    for (int i = 0; i < 4; ++i) sxr[i] = (4 * g + i < nb) ? sx[b0 + 4 * g + i] : 0.0f;
+        for (int i = 0; i < 4; ++i) sxr[i] = (g == 0 && i < nb) ? qscl[i] : 0.0f;
+    } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sxr[i] = (4 * g + i < nb) ? sx[b0 + 4 * g + i] : 0.0f;
+    }
     const bool vec_out = ((ld & 3) == 0) && ((((uintptr_t)logits) & 15) == 0);
     // candidate state: the first tile's values, this lane's rows' bounds
     float y0[4] = {0.0f, 0.0f, 0.0f, 0.0f}, bnd[4] = {INFINITY, INFINITY, INFINITY, INFINITY};
@@ -3421,6 +3564,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
         for (int bit = 31; bit >= 0; --bit) {
 #pragma unroll
             for (int bb = 0; bb < 16; ++bb) {
+                if (bb >= nb) break;
                 const uint32_t cand = K[bb] | (1u << bit);
                 if (__popcll(__ballot(sk[bb] >= cand)) >= C.ks) K[bb] = cand;
             }
@@ -3433,7 +3577,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
         }
         have_bnd = true;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) cand_stage(CS, 4 * g + i, y0[i], v0, ok0[i] && y0[i] >= bnd[i]);
+        for (int i = 0; i < 4; ++i) cand_stage(CS, wv, 4 * g + i, y0[i], v0, ok0[i] && y0[i] >= bnd[i]);
     };
     v4i acc_c = {0, 0, 0, 0};  // a finished tile waiting for cand_tile
     float sw_c = 0.0f;
@@ -3481,7 +3625,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
         } else {
             if (!have_bnd) take_bound();
 #pragma unroll
-            for (int i = 0; i < 4; ++i) cand_stage(CS, 4 * g + i, y[i], v, ok[i] && y[i] >= bnd[i]);
+            for (int i = 0; i < 4; ++i) cand_stage(CS, wv, 4 * g + i, y[i], v, ok[i] && y[i] >= bnd[i]);
         }
         pend = false;
     };
@@ -3556,34 +3700,39 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
         }
         sw_cur = sw_next;
     };
-    for (int s = 0; s < nstep; s += 4) {
+    // four steps per trip with no branch between them (steps past the wave's
+    // own belong to rounds past its tiles: computed, never stored), so that
+    // the compiler's wait counts see every load of the trip; a wave stops
+    // after its own tiles
+    const int ntile_w = (tlo + wv < thi) ? (thi - tlo - wv + LMM_WAVES - 1) / LMM_WAVES : 0;
+    const int nstep_w = ntile_w * npass;
+    for (int s = 0; s < nstep_w; s += 4) {
         step(w0, w3);
-        if (s + 1 < nstep) step(w1, w0);
-        if (s + 2 < nstep) step(w2, w1);
-        if (s + 3 < nstep) step(w3, w2);
+        step(w1, w0);
+        step(w2, w1);
+        step(w3, w2);
         if (CAND && pend) cand_tile();
     }
     // a wave with one tile reads the slots at its end
     if (CAND && !have_bnd && tlo + wv < thi) take_bound();
     if (CAND) {
-        // the staged values go to their rows' lists
-        __syncthreads();
-        if (tid < nb) {
-            const int c = CS.cnt[tid];
-            const int put = min(c, CAND_ROW);
-            int base = 0;
-            int4 *hm = C.hmeta + (size_t)(b0 + tid) * HMETA_STRIDE;
-            if (put > 0) base = atomicAdd(&hm->x, put);
-            CS.base[tid] = base;
+        // this wave's staged values go to their rows' lists (lane l < nb
+        // reserves row l's places; the wave's own LDS writes are in order)
+        const int c = (lane < nb) ? CS.cnt[wv][lane] : 0;
+        const int put = min(c, CAND_ROW);
+        int base = 0;
+        if (lane < nb && put > 0) {
+            int4 *hm = C.hmeta + (size_t)(b0 + lane) * HMETA_STRIDE;
+            base = atomicAdd(&hm->x, put);
             if (c > CAND_ROW || base + put > C.hcap) atomicOr(&hm->w, 1);
         }
-        __syncthreads();
-        for (int e = tid; e < nb * CAND_ROW; e += 64 * LMM_WAVES) {
-            const int row = e / CAND_ROW, j = e - row * CAND_ROW;
-            const int pos = CS.base[row] + j;
-            if (j < min(CS.cnt[row], CAND_ROW) && pos < C.hcap) {
-                C.lval[(size_t)(b0 + row) * C.hcap + pos] = CS.val[e];
-                C.lidx[(size_t)(b0 + row) * C.hcap + pos] = CS.id[e];
+        for (int row = 0; row < nb; ++row) {
+            const int pr = __builtin_amdgcn_readlane(put, row), br = __builtin_amdgcn_readlane(base, row);
+            for (int j = lane; j < pr; j += 64) {
+                if (br + j < C.hcap) {
+                    C.lval[(size_t)(b0 + row) * C.hcap + br + j] = CS.val[wv][row * CAND_ROW + j];
+                    C.lidx[(size_t)(b0 + row) * C.hcap + br + j] = CS.id[wv][row * CAND_ROW + j];
+                }
             }
         }
     }
@@ -4703,7 +4852,7 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
         const dim3 g2(nwg), blk(64 * LMM_WAVES);
         if (xres) {
             hipLaunchKernelGGL(lm_head_packed_xres_kernel<false>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab,
-                               d_logits, ld, b0, nb, HeadCand{});
+                               d_logits, ld, b0, nb, HeadCand{}, HeadQuant{});
             LAL_HIP(hipGetLastError());
             continue;
         }
@@ -4738,8 +4887,7 @@ int lal_gpu_lm_head_sample(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
     lal_gpu_sample_io sio = *io;
     sio.logits = d_logits;
     sio.ld = ld;
-    int rc = lal_gpu_quantize_x(ctx, d_x, batch, n, 0, d_xq, d_sx, stream);
-    if (rc != LAL_GPU_OK) return rc;
+    int rc = LAL_GPU_OK;
     // candidate lists from the head: up to 16 rows (activations resident),
     // no bias or allow mask (the list holds raw logits), and a sample bound
     // (ks <= 64 slots) for the row's k
@@ -4755,6 +4903,12 @@ int lal_gpu_lm_head_sample(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
     // tile per group of four steps waits for the candidate code)
     const bool cand = batch <= 16 && n <= LMX_MAXN && n > 3 * LMM_KC && ctx->lmh_xres != 0 && !io->allow_bits &&
                       !io->bias && ks <= 64 && k_eff <= LAL_GPU_MAX_K;
+    // up to QX_ROWS rows the head quantizes the activations itself
+    const bool qx_in = cand && batch <= QX_ROWS && ((uintptr_t)d_x & 15) == 0;
+    if (!qx_in) {
+        rc = lal_gpu_quantize_x(ctx, d_x, batch, n, 0, d_xq, d_sx, stream);
+        if (rc != LAL_GPU_OK) return rc;
+    }
     if (!cand) {
         rc = lal_gpu_lm_head_q8_packed(ctx, d_xq, d_sx, batch, n, d_wpk, d_sw, vocab, d_logits, ld, stream);
         if (rc != LAL_GPU_OK) return rc;
@@ -4767,8 +4921,12 @@ int lal_gpu_lm_head_sample(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
     C.lidx = ctx->lst_idx;
     C.hcap = FLAT_MAX;
     C.ks = ks;
+    HeadQuant HQ;
+    HQ.x = qx_in ? d_x : nullptr;
+    HQ.xq = d_xq;
+    HQ.sx = d_sx;
     hipLaunchKernelGGL(lm_head_packed_xres_kernel<true>, dim3(nwg), dim3(64 * LMM_WAVES), 0, (hipStream_t)stream,
-                       d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, 0, batch, C);
+                       d_xq, d_sx, n, d_wpk, d_sw, vocab, d_logits, ld, 0, batch, C, HQ);
     LAL_HIP(hipGetLastError());
     ListTarget t;
     t.ncu = ctx->ncu;

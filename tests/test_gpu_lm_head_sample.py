@@ -137,6 +137,7 @@ def fused_step(dev, dpk, dsw, V, n, x, hist, u, T=0.7, k=40, pen=1.1, top_p=0.0,
     res["cand_kept"] = bufs["ckept"].download((B, cand_ld), np.uint8)
     logits = bufs["logits"].download((B, V), np.float32)
     xq = bufs["xq"].download((B, n), np.int8)
+    res["sx_q"] = bufs["sx"].download(B, np.float32)
     for b in bufs.values():
         b.close()
     return logits, xq, res
@@ -209,6 +210,7 @@ def small_case(dev, orc, h, x, kw):
     for b in range(B):
         sx, xqo = orc.quantize_x(x[b].copy(), 0)
         assert np.array_equal(xqo, xq[b])
+        assert np.float32(sx).view(np.uint32) == got["sx_q"][b].view(np.uint32)
         want_logits[b] = orc.lm_head(xqo, sx, h["W"], h["sw"])
     assert np.array_equal(logits.view(np.uint32), want_logits.view(np.uint32))
     want = oracle_run(orc, want_logits, hist=hist, u=u, cand_ld=64, **kw)
@@ -232,6 +234,18 @@ def test_fused_nan_activation(dev, orc, small_heads):
     whole (the reference heap's nan semantics), the others use their lists."""
     x = (synth.normal(7400, 0, 4 * NS).reshape(4, NS)).astype(np.float32)
     x[2, 17] = np.float32(np.nan)
+    small_case(dev, orc, small_heads["random"], x, dict(T=0.8, k=5, pen=1.1))
+
+
+@pytest.mark.parametrize("B", [1, 3])
+def test_fused_quantize_in_head(dev, orc, small_heads, B):
+    """Up to four rows the head quantizes the activations itself: xq, sx and
+    the logits bit-exact with the oracle's quantizer, including a row with an
+    infinity and one with a nan (the AVX2 build's maximum order)."""
+    x = (synth.normal(7600 + B, 0, B * NS).reshape(B, NS) * np.float32(1.5)).astype(np.float32)
+    if B == 3:
+        x[1, 100] = np.float32(np.inf)
+        x[2, NS - 1] = np.float32(np.nan)
     small_case(dev, orc, small_heads["random"], x, dict(T=0.8, k=5, pen=1.1))
 
 
