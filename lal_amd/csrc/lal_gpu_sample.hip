@@ -319,6 +319,7 @@ struct KArgs {
     unsigned *hslots;
     int hcap;
     int hks;            // rank of the head's bound among the 64 slots
+    int prio_rotate;    // rotate the stream's wave priority over the CU's four workgroups
     int ncu;            // compute units: workgroups [3*ncu, 4*ncu) are the
                         // fourth (youngest) resident on their CU
 };
@@ -555,6 +556,7 @@ struct RowCtx {
     float pen;
     bool has_bias, has_allow, use_hash;
     bool bound_bias;  // bounds may carry the bias maximum in place of bias[e]
+    const uint32_t *bias_bits;  // ... for the ids whose bit is set here
 };
 
 // exact value of id e from its upper bound yhat, given its hash slot s (-1:
@@ -562,7 +564,9 @@ struct RowCtx {
 // maximum)
 __device__ __forceinline__ float exact_at_slot(const RowCtx &R, int e, float yhat, int s)
 {
-    if (s < 0 && !R.bound_bias) return yhat;
+    // outside the hash the bound is exact unless it carries the bias maximum
+    // (the id's bias bit is set; the map is small and cached, the row is not)
+    if (s < 0 && (!R.bound_bias || !((R.bias_bits[e >> 5] >> (e & 31)) & 1u))) return yhat;
     const int info = (s >= 0) ? R.hinfo[s] : 0;
     // without a bias the upper bound is the raw logit (or -inf when the allow
     // bit is clear, which the mask below keeps)
@@ -1745,11 +1749,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
         b = gi * 8 + (r & 7);
     }
     if (b >= A.batch) return;
-    // The youngest of the four workgroups resident on a CU loses the vector
-    // memory issue arbitration to the older three (which prefers older waves)
-    // and streams its row ~9% slower, setting the kernel's end; one priority
-    // step for its waves evens the four out.
-    if ((int)blockIdx.x / A.ncu == 3) __builtin_amdgcn_s_setprio(1);
+    // The vector memory issue arbitration of a CU prefers older waves, so the
+    // four workgroups resident on a CU stream at different rates.  One
+    // priority step for the youngest (grid index in [3 ncu, 4 ncu)) sets the
+    // fastest end for one workgroup per row; with sliced rows (prio_rotate)
+    // the priority rotates over the four every four stream iterations
+    // instead, so that every slice of a row gets each rank in turn.
+    const int pslot = ((int)blockIdx.x / A.ncu) & 3;
+    if (!A.prio_rotate && pslot == 3) __builtin_amdgcn_s_setprio(1);
     const int tid = threadIdx.x;
     const int w = wave_id(), lane = lane_id();
     const int V = A.V;
@@ -1957,6 +1964,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
     R.has_allow = HAS_ALLOW;
     R.use_hash = use_hash;
     R.bound_bias = HAS_BIAS;
+    R.bias_bits = A.bias_bits;
 
     float *bv = S.cval + w * CAPW;
     int *bi = S.cidx + w * CAPW;
@@ -2032,6 +2040,17 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
         wave_offer<1, CAPW>(bv, bi, hist, R, x, pm, eb, -INFINITY, st, k, &S.tau_key);
     }
     for (int q0 = qb; q0 < qe; q0 += WITER) {
+        if (A.prio_rotate) {
+            const int itn = (q0 - qb) / WITER;
+            if ((itn & 3) == 0) {
+                switch ((pslot + (itn >> 2)) & 3) {
+                case 0: __builtin_amdgcn_s_setprio(0); break;
+                case 1: __builtin_amdgcn_s_setprio(1); break;
+                case 2: __builtin_amdgcn_s_setprio(2); break;
+                default: __builtin_amdgcn_s_setprio(3); break;
+                }
+            }
+        }
         // two iterations stay in flight while this one is filtered
         f32x4 nx2[U4];
         const uint32_t aw2 = HAS_ALLOW ? wload(abits, q0 + 2 * WITER) : 0u;
@@ -4302,6 +4321,7 @@ struct lal_gpu_ctx {
     int lmh_xres;       // LAL_GPU_LMH_XRES: 0 disables the resident-activation kernel
     int lmh_pd;         // LAL_GPU_LMH_PD: W steps in flight (2 or 3)
     int list_ks;        // LAL_GPU_LIST_KS: rank of lal_gpu_lm_head_sample's bound (0: from k)
+    int list_rows;      // LAL_GPU_LIST_ROWS: largest batch that uses the head's candidate lists
     // slice lists (see KArgs): max_batch x FLAT_MAX entries, metadata for up
     // to MAX_SLICES slices per row, one arrival counter per row (zeroed here,
     // reset by every row's finisher)
@@ -4389,6 +4409,10 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     if (const char *env = getenv("LAL_GPU_LMH_XRES")) c->lmh_xres = atoi(env) != 0;
     if (const char *env = getenv("LAL_GPU_LMH_PD")) c->lmh_pd = (atoi(env) == 3) ? 3 : 2;
     if (const char *env = getenv("LAL_GPU_LIST_KS")) c->list_ks = std::min(64, std::max(0, atoi(env)));
+    // measured at [152064, 3584]: the lists win up to 4 rows (with the head
+    // quantizing), the separate sampler from 5 rows on
+    c->list_rows = 4;
+    if (const char *env = getenv("LAL_GPU_LIST_ROWS")) c->list_rows = std::min(16, std::max(0, atoi(env)));
     const size_t nl = (size_t)max_batch * FLAT_MAX;
     hipError_t e = hipMalloc((void **)&c->lst_val, nl * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->lst_idx, nl * sizeof(int));
@@ -4567,6 +4591,10 @@ static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gp
     // true by choose_slices, checked so that the kernel's overflow branch
     // stays unreachable
     if (A.nslice > 1 && A.lcap <= k_eff) return LAL_GPU_E_RANGE;
+    // sliced batches that fill the GPU (measured: 512 x 152064 with 2 slices
+    // per row, 86.9 -> 83.9 us; one workgroup per row is faster with the
+    // fixed step)
+    A.prio_rotate = (A.nslice > 1 && batch >= 64) ? 1 : 0;
     A.lst_val = t.lst_val;
     A.lst_idx = t.lst_idx;
     A.lst_meta = t.lst_meta;
@@ -4901,8 +4929,8 @@ int lal_gpu_lm_head_sample(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
     const int ks = ctx->list_ks > 0 ? ctx->list_ks : (int)std::ceil(lam + 6.0 * std::sqrt(lam) + 6.0);
     // (a tile spans at least four 256-byte passes of k: at most one finished
     // tile per group of four steps waits for the candidate code)
-    const bool cand = batch <= 16 && n <= LMX_MAXN && n > 3 * LMM_KC && ctx->lmh_xres != 0 && !io->allow_bits &&
-                      !io->bias && ks <= 64 && k_eff <= LAL_GPU_MAX_K;
+    const bool cand = batch <= ctx->list_rows && n <= LMX_MAXN && n > 3 * LMM_KC && ctx->lmh_xres != 0 &&
+                      !io->allow_bits && !io->bias && ks <= 64 && k_eff <= LAL_GPU_MAX_K;
     // up to QX_ROWS rows the head quantizes the activations itself
     const bool qx_in = cand && batch <= QX_ROWS && ((uintptr_t)d_x & 15) == 0;
     if (!qx_in) {

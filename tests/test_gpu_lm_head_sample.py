@@ -25,10 +25,41 @@ V, N = 152064, 3584
 
 @pytest.fixture(scope="module")
 def dev():
+    """A context whose lal_gpu_lm_head_sample uses the head's candidate lists
+    up to 16 rows (LAL_GPU_LIST_ROWS, read at creation), so that the list path
+    is exercised at every batch the tests use."""
+    import os
     from lal_amd import abi
-    d = abi.Device(0, max_batch=64, max_vocab=V)
+    old = os.environ.get("LAL_GPU_LIST_ROWS")
+    os.environ["LAL_GPU_LIST_ROWS"] = "16"
+    try:
+        d = abi.Device(0, max_batch=64, max_vocab=V)
+    finally:
+        if old is None:
+            del os.environ["LAL_GPU_LIST_ROWS"]
+        else:
+            os.environ["LAL_GPU_LIST_ROWS"] = old
     yield d
     d.close()
+
+
+def test_default_list_rows_path(orc, head):
+    """With the default LAL_GPU_LIST_ROWS, 16 rows take the separate sampler
+    (and 1 row the lists): same results either way."""
+    from lal_amd import abi
+    d = abi.Device(0, max_batch=64, max_vocab=V)
+    try:
+        for B in (1, 16):
+            x = (synth.normal(6100 + B, 0, B * N).reshape(B, N)).astype(np.float32)
+            hist = synth.history(6200 + B, B, 64, V)
+            u = orc.uniforms(6300 + B, B)
+            logits, _, got = fused_step(d, head["dpk"], head["dsw"], V, N, x, hist, u)
+            want_logits = oracle_logits(orc, head, x, ("qwen", B))
+            assert np.array_equal(logits.view(np.uint32), want_logits.view(np.uint32))
+            assert_same(got, oracle_run(orc, want_logits, T=0.7, k=40, pen=1.1, hist=hist, u=u, cand_ld=64),
+                        cand_ld=64)
+    finally:
+        d.close()
 
 
 @pytest.fixture(scope="module")
@@ -255,6 +286,7 @@ def test_fused_bound_check_fails_over(monkeypatch, orc, small_heads):
     results do not change."""
     from lal_amd import abi
     monkeypatch.setenv("LAL_GPU_LIST_KS", "1")
+    monkeypatch.setenv("LAL_GPU_LIST_ROWS", "16")
     d = abi.Device(0, max_batch=64, max_vocab=V)
     try:
         x = (synth.normal(7500, 0, 8 * NS).reshape(8, NS)).astype(np.float32)
