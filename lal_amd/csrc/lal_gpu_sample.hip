@@ -4635,7 +4635,7 @@ static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gp
 // ---- the sampler without allocation ---------------------------------------
 // Candidate lists and arrival counters of up to LAL_GPU_NOALLOC_MAX_ROWS sliced
 // rows, in one file-scope device array: each GPU the library runs on holds its
-// own copy (about 4.3 MB) until the process ends.  Host code never uses the
+// own copy (about 4.4 MB) until the process ends.  Host code never uses the
 // array's name as an address: its device address comes from
 // hipGetSymbolAddress, once per device, with that device current.
 struct NoallocScratch {
