@@ -3266,6 +3266,217 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_kernel(const in
     }
 }
 
+// Int8 LM head over the packed layout for 33..64 batch rows with the
+// activations resident in LDS.  k is split into two halves that the same
+// workgroup (8 waves, one per CU) runs one after the other: half h of the
+// batch's activations (MT*16 rows x at most 2 KB) is staged in LDS in
+// A-operand order (the slot rotation of lm_head_packed_kernel), every wave
+// streams W for its tiles with three steps in flight and no barrier per step,
+// and it keeps each tile's first-half int32 sums in registers (at most
+// LMK_MAXT tiles per wave) until its second pass over the tile adds the rest
+// (integer sums are exact in any order).  W is read once and the activations
+// twice per workgroup, instead of once per step.  Same arithmetic as
+// lm_head_packed_kernel: logits = (sx*sw)*(float)dot.
+//
+// Dynamic LDS (lmk_lds_bytes): xs [4*P0 k-blocks][MT][64 slots][16 B], then
+// per wave one finished tile (MT*16 rows x 16 floats), then the batch rows'
+// sx and the workgroup's tiles' sw.
+constexpr int LMK_WAVES = 8;
+constexpr int LMK_MAXT = 5;  // tiles per wave (the host checks the workgroups' share)
+constexpr int LMK_SWS = LMK_MAXT * LMK_WAVES * 16;
+constexpr int LMK_XPT = 16;  // staged 16-byte chunks per thread: 64 rows x 8 passes x 256 B / 512 threads
+
+__host__ __device__ constexpr size_t lmk_lds_bytes(int mt, int P0)
+{
+    return (size_t)4 * P0 * mt * 1024 + (size_t)LMK_WAVES * mt * 1024 + 64 * 4 + LMK_SWS * 4;
+}
+
+template <int MT>
+__global__ __launch_bounds__(64 * LMK_WAVES) void lm_head_ksplit_kernel(const int8_t *xq, const float *sx, int n,
+                                                                         const int8_t *wpk, const float *sw, int V,
+                                                                         float *logits, int ld, int b0, int nb)
+{
+    extern __shared__ __align__(16) int8_t lmk_smem[];
+    const int wv = wave_id(), lane = lane_id(), tid = threadIdx.x;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int nc64 = (n + 63) / 64;
+    const int npass = (nc64 + 3) / 4;
+    const int P0 = (npass + 1) / 2;  // passes of the first half (the second has npass - P0 <= P0)
+    int8_t *xs = lmk_smem;
+    float *o = reinterpret_cast<float *>(lmk_smem + (size_t)4 * P0 * MT * 1024) + wv * MT * 256;
+    float *sxs = reinterpret_cast<float *>(lmk_smem + (size_t)4 * P0 * MT * 1024 + LMK_WAVES * MT * 1024);
+    float *sws = sxs + 64;
+    const int ntile = (V + 15) / 16;
+    const int tlo = (int)(((long long)ntile * blockIdx.x) / gridDim.x);
+    const int thi = (int)(((long long)ntile * (blockIdx.x + 1)) / gridDim.x);
+    const int ntile_w = (tlo + wv < thi) ? (thi - tlo - wv + LMK_WAVES - 1) / LMK_WAVES : 0;
+
+    // the scales in LDS: the batch rows' sx, the workgroup's tiles' sw (read
+    // where a tile is finished, not carried in registers)
+    if (tid < 64) sxs[tid] = (tid < nb) ? sx[b0 + tid] : 0.0f;
+    for (int i = tid; i < (thi - tlo) * 16; i += 64 * LMK_WAVES) {
+        const int v = 16 * tlo + i;
+        sws[i] = (v < V) ? sw[v] : 0.0f;
+    }
+    const bool vec_out = ((ld & 3) == 0) && ((((uintptr_t)logits) & 15) == 0);
+    v4i saved[LMK_MAXT][MT];  // first-half sums of the wave's tiles
+#pragma unroll
+    for (int t = 0; t < LMK_MAXT; ++t)
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) saved[t][mt] = v4i{0, 0, 0, 0};
+
+    for (int h = 0; h < 2; ++h) {
+        const int pb = h ? P0 : 0;           // first pass of the half
+        const int ph = h ? npass - P0 : P0;  // passes of the half
+        // w of (round r, pass p of the half): this wave's tile, its blocks
+        // 4 (pb + p) .. +3, every load issued (clamped; products past n meet
+        // zero activations, padding steps are never stored)
+        auto fetch_w = [&](v4i (&f)[4], int r, int p) {
+            const int T = min(tlo + min(r, max(ntile_w, 1) - 1) * LMK_WAVES + wv, ntile - 1);
+            const v4i *base = reinterpret_cast<const v4i *>(wpk + ((size_t)T * nc64) * 1024) + lane;
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int c = min(4 * (pb + p) + s4, nc64 - 1);
+                f[s4] = __builtin_nontemporal_load(base + (size_t)c * 64);
+            }
+        };
+        // stage half h: chunk c = (row, c16), 16 bytes at k = 256 pb + 16 c16.
+        // All of a thread's chunks are loaded at once (every load issued, at
+        // a clamped address), then the first three steps' W, then the chunks
+        // go to LDS: one round trip for the staging, overlapped with W.
+        const int cph = 16 * ph;  // 16-byte chunks per row in the half
+        v4i xr[LMK_XPT];
+#pragma unroll
+        for (int j = 0; j < LMK_XPT; ++j) {
+            const int c = tid + j * 64 * LMK_WAVES;
+            const int row = c / cph, k = 256 * pb + 16 * (c - row * cph);
+            const bool in = c < MT * 16 * cph && row < nb && k < n;
+            const v4i v = *reinterpret_cast<const v4i *>(xq + (in ? (size_t)(b0 + row) * n + k : 0));
+            xr[j] = in ? v : v4i{0, 0, 0, 0};
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        v4i w0[4], w1[4], w2[4], w3[4];
+        int rw = 0, pw = 0;
+        auto advance = [&]() {
+            if (++pw == ph) { pw = 0; ++rw; }
+        };
+        // issued in step order (the scheduler would otherwise reorder them,
+        // and the loop's first wait would then cover every load in flight)
+        fetch_w(w0, rw, pw);
+        advance();
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_w(w1, rw, pw);
+        advance();
+        __builtin_amdgcn_sched_barrier(0);
+        fetch_w(w2, rw, pw);
+        advance();
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();  // the previous half's readers are done
+#pragma unroll
+        for (int j = 0; j < LMK_XPT; ++j) {
+            const int c = tid + j * 64 * LMK_WAVES;
+            if (c < MT * 16 * cph) {
+                const int row = c / cph, c16 = c - row * cph;
+                const int gg = c16 & 3, kb = c16 >> 2;
+                const int slot = gg * 16 + (((row & 15) + gg + 4 * (kb & 3)) & 15);
+                *reinterpret_cast<v4i *>(&xs[((kb * MT + (row >> 4)) * 64 + slot) * 16]) = xr[j];
+            }
+        }
+        __syncthreads();
+        if (ntile_w == 0) continue;
+
+        v4i acc[MT];
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt) acc[mt] = h ? saved[0][mt] : v4i{0, 0, 0, 0};
+        int r = 0, p = 0;
+        // a tile whose second half ended in this trip of four steps waits in
+        // LDS (scaled) and is stored at the trip's end (ph >= 4: at most one
+        // per trip), so that the unrolled steps make no global access but
+        // their W loads and the compiler's wait counts see every load in
+        // flight
+        int r_c = 0;
+        bool pend = false;
+        auto step = [&](v4i (&wc)[4], v4i (&wn)[4]) __attribute__((always_inline)) {
+            fetch_w(wn, rw, pw);
+            advance();
+#pragma unroll
+            for (int s4 = 0; s4 < 4; ++s4) {
+                const int slot = g * 16 + ((r16 + g + 4 * s4) & 15);
+#pragma unroll
+                for (int mt = 0; mt < MT; ++mt) {
+                    const v4i a = *reinterpret_cast<const v4i *>(xs + (((4 * p + s4) * MT + mt) * 64 + slot) * 16);
+                    acc[mt] = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, wc[s4], acc[mt], 0, 0, 0);
+                }
+            }
+            if (++p == ph) {  // this half of the tile is done
+                if (h == 0) {
+#pragma unroll
+                    for (int t = 0; t < LMK_MAXT; ++t)
+                        if (t == r)
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt) saved[t][mt] = acc[mt];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+                } else {
+                    const float swv = sws[(r * LMK_WAVES + wv) * 16 + r16];
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) {
+                        const f32x4 s4v = *reinterpret_cast<const f32x4 *>(sxs + mt * 16 + 4 * g);
+#pragma unroll
+                        for (int i = 0; i < 4; ++i)
+                            o[(mt * 16 + 4 * g + i) * 16 + r16] = (s4v[i] * swv) * (float)acc[mt][i];
+                    }
+                    r_c = r;
+                    pend = true;
+                    // the next tile starts from its first-half sums
+#pragma unroll
+                    for (int mt = 0; mt < MT; ++mt) acc[mt] = v4i{0, 0, 0, 0};
+#pragma unroll
+                    for (int t = 1; t < LMK_MAXT; ++t)
+                        if (t == r + 1)
+#pragma unroll
+                            for (int mt = 0; mt < MT; ++mt) acc[mt] = saved[t][mt];
+                }
+                ++r;
+                p = 0;
+            }
+        };
+        // tile r_c from LDS: lane l stores row 16 mt + l/4, vocab 16T +
+        // 4(l%4) .. +3 (one 16-byte store per 16-row block)
+        auto store_tile = [&]() __attribute__((always_inline)) {
+            const int T = tlo + r_c * LMK_WAVES + wv;
+            wave_sync();
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt) {
+                const int R = mt * 16 + (lane >> 2), v0 = 16 * T + 4 * (lane & 3);
+                const f32x4 val = *reinterpret_cast<const f32x4 *>(o + (mt * 16 + (lane >> 2)) * 16 + 4 * (lane & 3));
+                if (R < nb && T < thi) {
+                    float *dst = logits + (size_t)(b0 + R) * ld + v0;
+                    if (vec_out && v0 + 3 < V) {
+                        *reinterpret_cast<f32x4 *>(dst) = val;
+                    } else {
+#pragma unroll
+                        for (int c = 0; c < 4; ++c)
+                            if (v0 + c < V) dst[c] = val[c];
+                    }
+                }
+            }
+            wave_sync();  // read before the next tile overwrites it
+        };
+        const int nstep_w = ntile_w * ph;
+        for (int s = 0; s < nstep_w; s += 4) {
+            step(w0, w3);
+            step(w1, w0);
+            step(w2, w1);
+            step(w3, w2);
+            if (pend) {
+                store_tile();
+                pend = false;
+            }
+        }
+    }
+}
+
 // Startup weight quantizer (runtime/lal_q8_kernel.h:357-372,
 // lal_quantize_q8_per_row): per row, scale = max|w| / 127 (at least 1e-8),
 // q = lroundf(w * (1/scale)) clamped to [-127, 127] (round half away from
@@ -4322,6 +4533,7 @@ struct lal_gpu_ctx {
     int lmh_pd;         // LAL_GPU_LMH_PD: W steps in flight (2 or 3)
     int list_ks;        // LAL_GPU_LIST_KS: rank of lal_gpu_lm_head_sample's bound (0: from k)
     int list_rows;      // LAL_GPU_LIST_ROWS: largest batch that uses the head's candidate lists
+    int lmh_ksplit;     // LAL_GPU_LMH_KSPLIT: 0 disables the k-split head for 33..64 rows
     // slice lists (see KArgs): max_batch x FLAT_MAX entries, metadata for up
     // to MAX_SLICES slices per row, one arrival counter per row (zeroed here,
     // reset by every row's finisher)
@@ -4412,6 +4624,13 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     // measured at [152064, 3584]: the lists win up to 4 rows (with the head
     // quantizing), the separate sampler from 5 rows on
     c->list_rows = 4;
+    // the k-split head's dynamic LDS goes past 64 KB
+    c->lmh_ksplit = hipFuncSetAttribute((const void *)lm_head_ksplit_kernel<3>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess &&
+                    hipFuncSetAttribute((const void *)lm_head_ksplit_kernel<4>,
+                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess;
+    (void)hipGetLastError();
+    if (const char *env = getenv("LAL_GPU_LMH_KSPLIT")) c->lmh_ksplit = c->lmh_ksplit && atoi(env) != 0;
     if (const char *env = getenv("LAL_GPU_LIST_ROWS")) c->list_rows = std::min(16, std::max(0, atoi(env)));
     const size_t nl = (size_t)max_batch * FLAT_MAX;
     hipError_t e = hipMalloc((void **)&c->lst_val, nl * sizeof(float));
@@ -4881,6 +5100,26 @@ int lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float 
         if (xres) {
             hipLaunchKernelGGL(lm_head_packed_xres_kernel<false>, g2, blk, 0, s, d_xq, d_sx, n, d_wpk, d_sw, vocab,
                                d_logits, ld, b0, nb, HeadCand{}, HeadQuant{});
+            LAL_HIP(hipGetLastError());
+            continue;
+        }
+        // 33..64 rows: k split in two halves with the activations resident
+        // (one workgroup of 8 waves per CU); each half at least four passes
+        // of 256 k-bytes, every workgroup's share of tiles within LMK_MAXT
+        // per wave, the LDS within the CU's 160 KB
+        const int kwg = ctx->ncu;
+        const int npass = (n + LMM_KC - 1) / LMM_KC, P0 = (npass + 1) / 2;
+        const size_t klds = lmk_lds_bytes(mt, P0);
+        const bool ksplit = ctx->lmh_ksplit && mt >= 3 && npass - P0 >= 4 && klds <= 160 * 1024 &&
+                            mt * 16 * 16 * P0 <= LMK_XPT * 64 * LMK_WAVES &&
+                            (ntile + kwg - 1) / kwg <= LMK_MAXT * LMK_WAVES;
+        if (ksplit) {
+            if (mt == 3)
+                hipLaunchKernelGGL(lm_head_ksplit_kernel<3>, dim3(kwg), dim3(64 * LMK_WAVES), klds, s, d_xq, d_sx,
+                                   n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb);
+            else
+                hipLaunchKernelGGL(lm_head_ksplit_kernel<4>, dim3(kwg), dim3(64 * LMK_WAVES), klds, s, d_xq, d_sx,
+                                   n, d_wpk, d_sw, vocab, d_logits, ld, b0, nb);
             LAL_HIP(hipGetLastError());
             continue;
         }

@@ -74,19 +74,20 @@ def packed_layout(W):
     return Wp.reshape(NT, 16, NC, 4, 16).transpose(0, 2, 3, 1, 4).reshape(-1)
 
 
-def lm_head_packed(dev, xq, sx, W, sw):
+def lm_head_packed(dev, xq, sx, W, sw, ld=None):
     from lal_amd import abi
     B, n = xq.shape
     V = W.shape[0]
+    ld = V if ld is None else ld
     nbytes = dev.lib.lal_gpu_q8_packed_bytes(V, n)
     dW, dP = dev.put(np.ascontiguousarray(W)), dev.alloc(nbytes)
     abi.check(dev.lib.lal_gpu_pack_q8(dev.ctx, dW.ptr, V, n, dP.ptr, dev.stream), "pack")
     dq, ds, dsw = dev.put(np.ascontiguousarray(xq)), dev.put(np.asarray(sx, np.float32)), dev.put(sw)
-    dl = dev.alloc(4 * B * V)
+    dl = dev.alloc(4 * B * ld)
     abi.check(dev.lib.lal_gpu_lm_head_q8_packed(dev.ctx, dq.ptr, ds.ptr, B, n, dP.ptr, dsw.ptr, V, dl.ptr,
-                                                V, dev.stream), "lm_head_packed")
+                                                ld, dev.stream), "lm_head_packed")
     dev.sync()
-    out = dl.download((B, V), np.float32)
+    out = dl.download((B, ld), np.float32)[:, :V].copy()
     packed = dP.download(nbytes, np.int8)
     for b in (dW, dP, dq, ds, dsw, dl):
         b.close()
@@ -220,6 +221,28 @@ def test_lm_head_packed_activation_widths(dev, orc, B, n):
         want = orc.lm_head(q[b].copy(), s[b], W, sw)
         assert np.array_equal(out[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
     log(f"packed lm_head B={B} n={n}: bit-exact")
+
+
+@pytest.mark.parametrize("B,n,V,ld", [(40, 1808, 5003, 5003), (64, 2320, 4099, 4101), (48, 4096, 2051, 2052),
+                                      (33, 3600, 7001, 7001), (64, 3584, 9001, 9001), (64, 4096, 3001, 3001)])
+def test_lm_head_packed_ksplit_shapes(dev, orc, B, n, V, ld):
+    """33..64 rows split k in two halves per workgroup when each half has at
+    least four 256-byte passes and the LDS fits: the smallest split (n = 1808:
+    4 + 4 passes, the last one 16 bytes wide), halves of five passes (a tile
+    ends inside a trip of four steps), 16 and 15 passes at 33..48 rows, the
+    Qwen-7B width at 64 rows, and n = 4096 at 64 rows, whose LDS does not fit
+    (the per-step staging kernel); output rows that are not 16-byte aligned
+    (ld = 4101) and partial last 16-column tiles."""
+    rng = np.random.default_rng(3000 + B + n)
+    W = rng.integers(-127, 128, (V, n)).astype(np.int8)
+    sw = (rng.random(V) * 0.019 + 0.001).astype(np.float32)
+    x = synth.normal(370 + B, 0, B * n).reshape(B, n).astype(np.float32)
+    s, q = quantize(dev, x, 0)
+    out, _ = lm_head_packed(dev, q, s, W, sw, ld=ld)
+    for b in range(B):
+        want = orc.lm_head(q[b].copy(), s[b], W, sw)
+        assert np.array_equal(out[b].view(np.uint32), want.view(np.uint32)), f"row {b}"
+    log(f"packed lm_head B={B} n={n} V={V} ld={ld}: bit-exact")
 
 
 def test_pack_layout_ragged(dev):
