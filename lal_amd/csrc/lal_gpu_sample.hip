@@ -2893,6 +2893,138 @@ __global__ __launch_bounds__(256) void quantize_x_kernel(const float *x, int n, 
     if (t == 0) sx[b] = scale;
 }
 
+// quantize_x_kernel for rows of at most 4096 values, in one round trip: each
+// thread loads its values once (thread (segment s, lane j) holds x[8c + j]
+// for the chunks c of segment s, as qx_scale folds them), the per-lane folds
+// of the AVX2 build combine across segments with shuffles (the fold is
+// associative: a run that holds a nan replaces what precedes it, one without
+// keeps the earlier nan flag and takes the larger maximum), and the bytes
+// leave through LDS in 16-byte stores.  Same values as quantize_x_kernel.
+constexpr int QXF_MAXN = 4096;
+constexpr int QXF_PT = QXF_MAXN / 256;  // chunks per segment at most
+
+__global__ __launch_bounds__(256) void quantize_x_fast_kernel(const float *x, int n, int mode, int8_t *xq,
+                                                              float *sx)
+{
+    __shared__ float seg_m[4][8];
+    __shared__ int seg_f[4][8];
+    __shared__ float lane_m[8];
+    __shared__ float tailv[8];
+    __shared__ float red[4];
+    __shared__ __align__(16) int8_t qs[QXF_MAXN];
+    const int b = blockIdx.x, t = threadIdx.x, lane = lane_id(), wv = wave_id();
+    const float *xr = x + (size_t)b * n;
+    const int n8 = n & ~7, nch = n8 >> 3;
+    const int j = t & 7, sgi = t >> 3;
+    const int c0 = (int)(((long long)nch * sgi) / 32), c1 = (int)(((long long)nch * (sgi + 1)) / 32);
+    float v[QXF_PT];
+#pragma unroll
+    for (int u = 0; u < QXF_PT; ++u) v[u] = xr[min(8 * (c0 + u) + j, n - 1)];  // every load issued
+    const int ntail = n - n8;
+    const float tv = xr[min(n8 + min(t, 7), n - 1)];
+    if (t < ntail) tailv[t] = tv;
+    float m = 0.0f;
+    if (mode == 0) {
+        float acc = -1.0f;  // -1: no value after the last nan
+        int f = 0;          // 1: a nan seen, 2: the run ends in a nan, 4: the run has values
+#pragma unroll
+        for (int u = 0; u < QXF_PT; ++u) {
+            if (c0 + u < c1) {
+                const float a = fabsf(v[u]);
+                if (a != a) {
+                    f = 1 | 2 | 4;
+                    acc = -1.0f;
+                } else {
+                    f = (f & 1) | 4;
+                    acc = fmaxf(acc, a);
+                }
+            }
+        }
+        // segments 8w .. 8w+7 of lane j sit in lanes j, j+8, .., j+56 of wave
+        // w: fold them in order, the later run on the right
+#pragma unroll
+        for (int off = 8; off < 64; off <<= 1) {
+            const int rf = __shfl_down(f, off, 64);
+            const float racc = __shfl_down(acc, off, 64);
+            if ((lane & (2 * off - 1)) < 8 && (rf & 4)) {
+                if (rf & 1) {
+                    f = rf;
+                    acc = racc;
+                } else {
+                    f = (f & 1) | 4;
+                    acc = fmaxf(acc, racc);
+                }
+            }
+        }
+        if (lane < 8) {
+            seg_m[wv][lane] = acc;
+            seg_f[wv][lane] = f;
+        }
+        __syncthreads();
+        if (t < 8) {
+            float la = -1.0f;
+            int lf = 0;
+#pragma unroll
+            for (int w = 0; w < 4; ++w) {
+                const int ff = seg_f[w][t];
+                if (!(ff & 4)) continue;
+                if (ff & 1) {
+                    lf = ff;
+                    la = seg_m[w][t];
+                } else {
+                    lf = (lf & 1) | 4;
+                    la = fmaxf(la, seg_m[w][t]);
+                }
+            }
+            lane_m[t] = (lf & 2) ? __builtin_nanf("") : fmaxf(la, 0.0f);
+        }
+        __syncthreads();
+        if (t == 0) {
+            // the build's lane reduction (_mm256 halves, then shuffles), then
+            // the tail with `a > max`
+            float h[4];
+            for (int q = 0; q < 4; ++q) h[q] = x86_maxps(lane_m[q], lane_m[q + 4]);
+            const float s1[4] = {h[2], h[3], h[0], h[1]};
+            for (int q = 0; q < 4; ++q) h[q] = x86_maxps(h[q], s1[q]);
+            float mm = x86_maxps(h[0], h[1]);
+            for (int i = 0; i < ntail; ++i) {
+                const float a = fabsf(tailv[i]);
+                if (a > mm) mm = a;
+            }
+            red[0] = mm;
+        }
+        __syncthreads();
+        m = red[0];
+    } else {
+        // `a > max` over every value: order-free, never a nan
+#pragma unroll
+        for (int u = 0; u < QXF_PT; ++u)
+            if (c0 + u < c1) m = fmaxf(m, fabsf(v[u]));
+        if (t < ntail) m = fmaxf(m, fabsf(tv));
+        m = wave_max(m);
+        if (lane == 0) red[wv] = m;
+        __syncthreads();
+        m = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    }
+    float scale = m / 127.0f;
+    if (scale < 1e-8f) scale = 1e-8f;
+    const float inv = 1.0f / scale;
+    // mode 0 rounds the 8-wide prefix and truncates the tail; mode 1 truncates
+#pragma unroll
+    for (int u = 0; u < QXF_PT; ++u)
+        if (c0 + u < c1) qs[8 * (c0 + u) + j] = qx_value(v[u], inv, mode == 0);
+    if (t < ntail) qs[n8 + t] = qx_value(tv, inv, false);
+    __syncthreads();
+    int8_t *dst = xq + (size_t)b * n;
+    if ((n & 15) == 0 && (((uintptr_t)dst) & 15) == 0) {
+        for (int i = t; i < n / 16; i += 256)
+            reinterpret_cast<int4 *>(dst)[i] = reinterpret_cast<const int4 *>(qs)[i];
+    } else {
+        for (int i = t; i < n; i += 256) dst[i] = qs[i];
+    }
+    if (t == 0) sx[b] = scale;
+}
+
 // GEMV/GEMM-by-rows: each wave computes LMH_ROWS vocab rows for all batch rows
 // with v_dot4 int8 dot products (exact int32 accumulation).
 constexpr int LMH_ROWS = 4;
@@ -4984,8 +5116,12 @@ int lal_gpu_quantize_x(lal_gpu_ctx *ctx, const float *d_x, int batch, int n, int
 {
     if (!ctx || !d_x || !d_xq || !d_sx || batch <= 0 || n <= 0 || (mode != 0 && mode != 1))
         return LAL_GPU_E_INVAL;
-    hipLaunchKernelGGL(quantize_x_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, d_x, n,
-                       mode, d_xq, d_sx);
+    if (n <= QXF_MAXN)
+        hipLaunchKernelGGL(quantize_x_fast_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, d_x, n, mode,
+                           d_xq, d_sx);
+    else
+        hipLaunchKernelGGL(quantize_x_kernel, dim3(batch), dim3(256), 0, (hipStream_t)stream, d_x, n, mode,
+                           d_xq, d_sx);
     LAL_HIP(hipGetLastError());
     return LAL_GPU_OK;
 }

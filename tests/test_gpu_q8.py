@@ -116,6 +116,23 @@ def test_quantize_x_nan_inf(dev, orc):
             assert np.array_equal(q[0], qo), (len(x), mode, np.nonzero(q[0] != qo)[0][:8])
 
 
+@pytest.mark.parametrize("n", [1, 15, 100, 1000, 2049, 3584, 4096, 4097, 8000])
+def test_quantize_x_widths(dev, orc, n):
+    """Rows up to 4096 values take the one-round-trip quantizer, longer ones
+    the looped one: both modes against the oracle on every byte, a few rows
+    per call, widths with and without an 8-value tail."""
+    B = 5
+    x = (synth.normal(4400 + n, 0, B * n) * np.float32(2.5)).astype(np.float32).reshape(B, n)
+    x[1] *= np.float32(1e-12)  # the 1e-8 scale floor
+    for mode in (0, 1):
+        s, q = quantize(dev, x, mode)
+        for b in range(B):
+            so, qo = orc.quantize_x(x[b].copy(), mode)
+            assert s[b].view(np.uint32) == np.float32(so).view(np.uint32), (n, mode, b)
+            assert np.array_equal(q[b], qo), (n, mode, b)
+    log(f"quantize_x n={n}: {B} rows, both modes")
+
+
 def test_lm_head_golden(dev):
     for rec in golden_cases.load()["q8"]["lm_head"]:
         V, n, seed = rec["V"], rec["n"], rec["seed"]

@@ -46,7 +46,7 @@ def kernels(report, marker):
                                     "sample_rows_kernelILb1ELb0E", "sample_rows_kernelILb1ELb1E",
                                     "bias_prep_kernel", "lm_head_packed_kernel",
                                     "lm_head_packed_xres_kernel", "lm_head_ksplit_kernel", "finish_rows_kernel",
-                                    "quantize_x_kernel"])
+                                    "quantize_x_kernel", "quantize_x_fast_kernel"])
 def test_no_scratch(report, marker):
     bad = {k: v["ScratchSize"] for k, v in kernels(report, marker).items() if v.get("ScratchSize", 0) != 0}
     assert not bad, f"scratch spills (bytes/lane): {bad}"
