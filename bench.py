@@ -56,7 +56,7 @@ for _b in (1, 16):
                                                    top_p=0.0, pen=1.2, H=128, gpt2=True, rerank=512)
 
 
-DOMINANT = {"lmhead": "lm_head_packed_xres_kernel (B <= 16) / lm_head_packed_kernel",
+DOMINANT = {"lmhead": "lm_head_packed_xres_kernel (B <= 16) / lm_head_ksplit_kernel (B 33..64) / lm_head_packed_kernel",
             "gpt2lm": "lm_head_dot4_kernel + rerank_select_kernel"}
 
 

@@ -3464,11 +3464,15 @@ __global__ __launch_bounds__(64 * LMK_WAVES) void lm_head_ksplit_kernel(const in
         // 4 (pb + p) .. +3, every load issued (clamped; products past n meet
         // zero activations, padding steps are never stored)
         auto fetch_w = [&](v4i (&f)[4], int r, int p) {
-            const int T = min(tlo + min(r, max(ntile_w, 1) - 1) * LMK_WAVES + wv, ntile - 1);
+            // a step past the wave's tiles reads again the blocks of its last
+            // step of the half (just read: a cache hit)
+            const bool ok = r < ntile_w;
+            const int T = min(tlo + (ok ? r : max(ntile_w, 1) - 1) * LMK_WAVES + wv, ntile - 1);
+            const int pc = ok ? p : ph - 1;
             const v4i *base = reinterpret_cast<const v4i *>(wpk + ((size_t)T * nc64) * 1024) + lane;
 #pragma unroll
             for (int s4 = 0; s4 < 4; ++s4) {
-                const int c = min(4 * (pb + p) + s4, nc64 - 1);
+                const int c = min(4 * (pb + pc) + s4, nc64 - 1);
                 f[s4] = __builtin_nontemporal_load(base + (size_t)c * 64);
             }
         };
@@ -3731,19 +3735,23 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     const int nstep = nround * npass;
 
     // w of (round r, pass p): this wave's tile, blocks 4p .. 4p+3.  Every
-    // load is issued (a wave past its tiles reads its workgroup's first tile,
-    // blocks past the row read its last one): with no branch around them the
+    // load is issued (a wave past its tiles reads its last step's blocks
+    // again, blocks past the row read its last one): with no branch around them the
     // compiler counts the loads in flight exactly and waits only for the step
     // it multiplies.  The extra products are exact zeros (the activations of
     // blocks past n are zero in LDS) or belong to tiles that are not stored.
+    // this wave's tiles: tlo + wv + LMM_WAVES r for r < ntile_w
+    const int ntile_w = (tlo + wv < thi) ? (thi - tlo - wv + LMM_WAVES - 1) / LMM_WAVES : 0;
     auto fetch_w = [&](v4i (&f)[4], int r, int p) {
-        const int T = tlo + r * LMM_WAVES + wv;
-        const bool ok = r < nround && T < thi;
-        const int Tc = min(ok ? T : tlo, ntile - 1);
+        // a step past the wave's tiles reads again the blocks of its last
+        // step (just read: a cache hit), not blocks read long ago
+        const bool ok = r < ntile_w;
+        const int Tc = min(tlo + (ok ? r : max(ntile_w, 1) - 1) * LMM_WAVES + wv, ntile - 1);
+        const int pc = ok ? p : npass - 1;
         const v4i *base = reinterpret_cast<const v4i *>(wpk + ((size_t)Tc * nc64) * 1024) + lane;
 #pragma unroll
         for (int s4 = 0; s4 < 4; ++s4) {
-            const int c = min(4 * p + s4, nc64 - 1);
+            const int c = min(4 * pc + s4, nc64 - 1);
             f[s4] = __builtin_nontemporal_load(base + (size_t)c * 64);
         }
     };
@@ -4066,7 +4074,6 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     // own belong to rounds past its tiles: computed, never stored), so that
     // the compiler's wait counts see every load of the trip; a wave stops
     // after its own tiles
-    const int ntile_w = (tlo + wv < thi) ? (thi - tlo - wv + LMM_WAVES - 1) / LMM_WAVES : 0;
     const int nstep_w = ntile_w * npass;
     for (int s = 0; s < nstep_w; s += 4) {
         step(w0, w3);
