@@ -3679,6 +3679,8 @@ struct HeadCand {
 struct CandStage {
     unsigned wgmax[16];  // per-row maximum key of the workgroup's first tiles
     int done0;           // waves past their first tile
+    unsigned bkey[16];   // per-row bound key a wave of the workgroup took from the slots
+    int bready;          // bkey is set
     int cnt[LMM_WAVES][16];  // staged values per row (may exceed CAND_ROW: full)
     float val[LMM_WAVES][16 * CAND_ROW];
     int id[LMM_WAVES][16 * CAND_ROW];
@@ -3724,7 +3726,10 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     if (CAND) {
         if (tid < 16) CS.wgmax[tid] = 0u;
         if (tid < 16 * LMM_WAVES) CS.cnt[tid >> 4][tid & 15] = 0;
-        if (tid == 0) CS.done0 = 0;
+        if (tid == 0) {
+            CS.done0 = 0;
+            CS.bready = 0;
+        }
     }
     const int npass = (n + LMM_KC - 1) / LMM_KC;
     const int nc64 = (n + 63) / 64;  // 1 KB blocks per 16-row tile
@@ -3921,22 +3926,41 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     bool have_bnd = false;
     auto take_bound = [&]() __attribute__((always_inline)) {
         // the ks-th largest slot of every row, 16 rows side by side (bit by
-        // bit, ballot counts), then the first tile's values against it
-        uint32_t sk[16], K[16];
+        // bit, ballot counts), then the first tile's values against it.  The
+        // first wave of the workgroup to get here reads the slots (a global
+        // round trip that drains its W pipeline) and leaves the bounds in
+        // LDS; a later wave takes them from there.  Any wave's bound is at
+        // most the bound of the final slots (slots only grow), which the
+        // sampler checks the list against.
+        uint32_t K[16];
+        const int ready = __builtin_amdgcn_readfirstlane(
+            __hip_atomic_load(&CS.bready, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_WORKGROUP));
+        if (ready) {
 #pragma unroll
-        for (int bb = 0; bb < 16; ++bb) {
-            sk[bb] = (bb < nb) ? __hip_atomic_load(&C.hslots[(size_t)(b0 + bb) * 64 + lane], __ATOMIC_RELAXED,
-                                                   __HIP_MEMORY_SCOPE_AGENT)
-                               : 0u;
-            K[bb] = 0u;
-        }
-#pragma unroll 1
-        for (int bit = 31; bit >= 0; --bit) {
+            for (int bb = 0; bb < 16; ++bb) K[bb] = (bb < nb) ? CS.bkey[bb] : 0u;
+        } else {
+            uint32_t sk[16];
 #pragma unroll
             for (int bb = 0; bb < 16; ++bb) {
-                if (bb >= nb) break;
-                const uint32_t cand = K[bb] | (1u << bit);
-                if (__popcll(__ballot(sk[bb] >= cand)) >= C.ks) K[bb] = cand;
+                sk[bb] = (bb < nb) ? __hip_atomic_load(&C.hslots[(size_t)(b0 + bb) * 64 + lane], __ATOMIC_RELAXED,
+                                                       __HIP_MEMORY_SCOPE_AGENT)
+                                   : 0u;
+                K[bb] = 0u;
+            }
+#pragma unroll 1
+            for (int bit = 31; bit >= 0; --bit) {
+#pragma unroll
+                for (int bb = 0; bb < 16; ++bb) {
+                    if (bb >= nb) break;
+                    const uint32_t cand = K[bb] | (1u << bit);
+                    if (__popcll(__ballot(sk[bb] >= cand)) >= C.ks) K[bb] = cand;
+                }
+            }
+            if (lane == 0) {
+#pragma unroll
+                for (int bb = 0; bb < 16; ++bb)
+                    if (bb < nb) CS.bkey[bb] = K[bb];
+                __hip_atomic_store(&CS.bready, 1, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_WORKGROUP);
             }
         }
 #pragma unroll
