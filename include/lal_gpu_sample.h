@@ -250,14 +250,14 @@ int  lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float
  * sampler with params / io (io->logits and io->ld are ignored: the step's
  * logits are used).  Results are bit for bit those of lal_gpu_quantize_x +
  * lal_gpu_lm_head_q8_packed + lal_gpu_sample.  For up to LAL_GPU_LIST_ROWS
- * rows (default 4, at most 16) without a bias or allow mask the head
- * quantizes the activations itself (up to 4 rows) and keeps, per row, the
- * logits at or above a bound taken from a fixed sample of its tiles, and the
+ * rows (default 4, at most 16) without a bias or allow mask the head keeps,
+ * per row, the logits at or above a bound taken from a fixed sample of its
+ * tiles (with LAL_GPU_HEAD_QX=1 it also quantizes up to 4 rows itself), and the
  * sampler reads that list instead of the row; a row whose list cannot be
  * shown to hold its top-k pool (fewer than k values at or above the bound, a
  * nan logit, a full list) is read whole, as lal_gpu_sample reads it.
- * LAL_GPU_LIST_ROWS and LAL_GPU_LIST_KS (the bound's rank, for tests) are
- * read when the context is created.
+ * LAL_GPU_LIST_ROWS, LAL_GPU_HEAD_QX and LAL_GPU_LIST_KS (the bound's rank,
+ * for tests) are read when the context is created.
  * Needs n % 16 == 0, 16-byte aligned d_xq / d_wpk, batch <= max_batch and
  * vocab <= max_vocab of the context. */
 int  lal_gpu_lm_head_sample(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,

@@ -62,6 +62,8 @@ constexpr int K_SMALL_MAX = 128;
 constexpr int MAX_SLICES = 64;                 // slices per row
 constexpr int FLAT_MAX = NWAVE * CAPW_LARGE;   // slice-list entries per row
 constexpr int HMETA_STRIDE = 16;               // int4 per row of an LM head's list state (256 bytes)
+constexpr int HSUB = 8;                        // sub-lists per row of an LM head's candidates
+static_assert(HMETA_STRIDE >= 1 + HSUB, "list state: flags + sub-list counts");
 // row sample for the threshold estimate: 64 float4 (1 KB) every SBLK float4
 constexpr int SBLK = 2048;          // 32 KB stride -> 1/32 of the row
 constexpr int SR = 5;               // float4 per thread: up to 20 sampled blocks (V <= 163840 fully sampled)
@@ -311,10 +313,11 @@ struct KArgs {
     int4 *lst_meta;     // [batch][nslice] (count, threshold bits, strict, -)
     unsigned *arrive;   // [batch] slices finished; reset by the finisher
     // candidate lists an LM head wrote (list mode): row b's entries at
-    // lst_val / lst_idx + b * hcap, hmeta[b * HMETA_STRIDE] = (count, -, -,
-    // flags: 1 list full, 2 a nan logit), hslots[b][64] the sample slots the
-    // bound comes from (rank hks); both are cleared by the row's workgroup for
-    // the next head
+    // lst_val / lst_idx + b * hcap in HSUB sub-lists of hcap / HSUB entries,
+    // hmeta[b * HMETA_STRIDE] = (-, -, -, flags: 1 list full, 2 a nan logit),
+    // hmeta[b * HMETA_STRIDE + 1 + s].x = entries of sub-list s, hslots[b][64]
+    // the sample slots the bound comes from (rank hks); both are cleared by
+    // the row's workgroup for the next head
     int4 *hmeta;
     unsigned *hslots;
     int hcap;
@@ -1782,12 +1785,18 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
     // after the list pass); a full list, a nan logit or no bound: the row is
     // streamed
     int hcnt = 0;
+    int hsc[HSUB];  // entries of each sub-list
     uint32_t hkey = 0u;
     bool list_ok = false;
     if (LIST) {
         const int4 hm = A.hmeta[(size_t)b * HMETA_STRIDE];
-        hcnt = hm.x;
-        list_ok = (hm.w & 3) == 0 && hcnt >= 0 && hcnt <= A.hcap;
+        list_ok = (hm.w & 3) == 0;
+#pragma unroll
+        for (int q = 0; q < HSUB; ++q) {
+            hsc[q] = A.hmeta[(size_t)b * HMETA_STRIDE + 1 + q].x;
+            list_ok = list_ok && hsc[q] >= 0 && hsc[q] <= A.hcap / HSUB;
+            hcnt += hsc[q];
+        }
     }
 
     const RowGeo g = row_geo(row, V);
@@ -2009,16 +2018,25 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
 
     if (from_list) {
         // every list value is a raw logit of an id the head computed once;
-        // the waves take 64 entries at a time, in rotation
+        // the waves take 64 entries of the sub-lists' concatenation at a
+        // time, in rotation
         const float *lv = A.lst_val + (size_t)b * A.hcap;
         const int *li = A.lst_idx + (size_t)b * A.hcap;
+        const int subcap = A.hcap / HSUB;
         for (int j0 = w * 64; j0 < hcnt; j0 += NWAVE * 64) {
             const int j = j0 + lane;
+            int sq = 0, off = j;  // entry j: sub-list sq, entry off
+#pragma unroll
+            for (int q = 0; q < HSUB - 1; ++q)
+                if (sq == q && off >= hsc[q]) {
+                    off -= hsc[q];
+                    sq = q + 1;
+                }
             float x[4] = {NAN, NAN, NAN, NAN};
             int eb[1] = {0};
             if (j < hcnt) {
-                x[0] = lv[j];
-                eb[0] = li[j];
+                x[0] = lv[sq * subcap + off];
+                eb[0] = li[sq * subcap + off];
             }
             const float tsh = keyf(S.tau_key);
             const float tcmp = (st.tcmp != st.tcmp) ? st.tcmp : fmaxf(st.tcmp, tsh);
@@ -2175,7 +2193,7 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
     if (LIST) {
         // the head's per-row state starts from zero at its next launch
         if (tid < 64) A.hslots[(size_t)b * 64 + tid] = 0u;
-        if (tid == 0) A.hmeta[(size_t)b * HMETA_STRIDE] = int4{0, 0, 0, 0};
+        if (tid <= HSUB) A.hmeta[(size_t)b * HMETA_STRIDE + tid] = int4{0, 0, 0, 0};
     }
 
     // Past the stream.  The arguments are read again from the kernel argument
@@ -3660,13 +3678,15 @@ __global__ __launch_bounds__(256) void quantize_w_kernel(const float *w, int n, 
 // list values at or above it), streaming the row otherwise.  A wave reads the
 // slots after its second tile (or its only one) and filters its first tile's
 // values then.  Passing values are staged per wave in LDS (CAND_ROW per row:
-// about 200 of a row's values pass over some 2000 waves) and written out by
-// the wave at its end, one atomic per row reserving their place in the row's
-// list.  A nan logit or a full stage or list flags the row.
+// about 200 of a row's values pass over some 2000 waves); the last wave of a
+// workgroup to finish writes every wave's values out, one atomic per row
+// reserving their place in sub-list (workgroup index % HSUB) of the row's
+// list (one counter for all 512 workgroups serialised ~2000 atomics at the
+// kernel's end).  A nan logit or a full stage or list flags the row.
 constexpr int CAND_ROW = 8;
 constexpr int LMX_MAXN = 4096;
 struct HeadCand {
-    int4 *hmeta;      // [row * HMETA_STRIDE] (count, -, -, flags: 1 full, 2 nan)
+    int4 *hmeta;      // [row * HMETA_STRIDE] (-, -, -, flags: 1 full, 2 nan), then HSUB sub-list counts
     unsigned *hslots; // [row][64]
     float *lval;      // [row][hcap]
     int *lidx;
@@ -3679,6 +3699,7 @@ struct HeadCand {
 struct CandStage {
     unsigned wgmax[16];  // per-row maximum key of the workgroup's first tiles
     int done0;           // waves past their first tile
+    int done_end;        // waves past their last tile
     unsigned bkey[16];   // per-row bound key a wave of the workgroup took from the slots
     int bready;          // bkey is set
     int cnt[LMM_WAVES][16];  // staged values per row (may exceed CAND_ROW: full)
@@ -3728,6 +3749,7 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
         if (tid < 16 * LMM_WAVES) CS.cnt[tid >> 4][tid & 15] = 0;
         if (tid == 0) {
             CS.done0 = 0;
+            CS.done_end = 0;
             CS.bready = 0;
         }
     }
@@ -4109,22 +4131,50 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
     // a wave with one tile reads the slots at its end
     if (CAND && !have_bnd && tlo + wv < thi) take_bound();
     if (CAND) {
-        // this wave's staged values go to their rows' lists (lane l < nb
-        // reserves row l's places; the wave's own LDS writes are in order)
-        const int c = (lane < nb) ? CS.cnt[wv][lane] : 0;
-        const int put = min(c, CAND_ROW);
+        // the last wave of the workgroup to get here writes every wave's
+        // staged values to sub-list (blockIdx % HSUB) of their rows: lane
+        // l < nb reserves row l's places with one atomic (the waves' LDS
+        // writes are ordered before their arrival by the release / acquire)
+        int prev = 0;
+        if (lane == 0)
+            prev = __hip_atomic_fetch_add(&CS.done_end, 1, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_WORKGROUP);
+        prev = __builtin_amdgcn_readfirstlane(prev);
+        if (prev != LMM_WAVES - 1) return;
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        int putw[LMM_WAVES];
+        int tot = 0;
+        bool over = false;
+#pragma unroll
+        for (int ww = 0; ww < LMM_WAVES; ++ww) {
+            const int c = (lane < nb) ? CS.cnt[ww][lane] : 0;
+            putw[ww] = min(c, CAND_ROW);
+            tot += putw[ww];
+            over = over || c > CAND_ROW;
+        }
+        const int sq = (int)(blockIdx.x % HSUB), subcap = C.hcap / HSUB;
         int base = 0;
-        if (lane < nb && put > 0) {
+        if (lane < nb && tot > 0) {
             int4 *hm = C.hmeta + (size_t)(b0 + lane) * HMETA_STRIDE;
-            base = atomicAdd(&hm->x, put);
-            if (c > CAND_ROW || base + put > C.hcap) atomicOr(&hm->w, 1);
+            base = atomicAdd(&hm[1 + sq].x, tot);
+            if (over || base + tot > subcap) atomicOr(&hm->w, 1);
         }
         for (int row = 0; row < nb; ++row) {
-            const int pr = __builtin_amdgcn_readlane(put, row), br = __builtin_amdgcn_readlane(base, row);
-            for (int j = lane; j < pr; j += 64) {
-                if (br + j < C.hcap) {
-                    C.lval[(size_t)(b0 + row) * C.hcap + br + j] = CS.val[wv][row * CAND_ROW + j];
-                    C.lidx[(size_t)(b0 + row) * C.hcap + br + j] = CS.id[wv][row * CAND_ROW + j];
+            const int tr = __builtin_amdgcn_readlane(tot, row), br = __builtin_amdgcn_readlane(base, row);
+            for (int j = lane; j < tr; j += 64) {
+                // entry j of the row: wave ww's staged value jj
+                int ww = 0, jj = j;
+#pragma unroll
+                for (int q = 0; q < LMM_WAVES - 1; ++q) {
+                    const int pq = __builtin_amdgcn_readlane(putw[q], row);
+                    if (ww == q && jj >= pq) {
+                        jj -= pq;
+                        ww = q + 1;
+                    }
+                }
+                if (br + j < subcap) {
+                    const size_t o = (size_t)(b0 + row) * C.hcap + (size_t)sq * subcap + br + j;
+                    C.lval[o] = CS.val[ww][row * CAND_ROW + jj];
+                    C.lidx[o] = CS.id[ww][row * CAND_ROW + jj];
                 }
             }
         }
@@ -4697,6 +4747,7 @@ struct lal_gpu_ctx {
     int list_ks;        // LAL_GPU_LIST_KS: rank of lal_gpu_lm_head_sample's bound (0: from k)
     int list_rows;      // LAL_GPU_LIST_ROWS: largest batch that uses the head's candidate lists
     int lmh_ksplit;     // LAL_GPU_LMH_KSPLIT: 0 disables the k-split head for 33..64 rows
+    int head_qx;        // LAL_GPU_HEAD_QX: 1 lets the candidate head quantize up to 4 rows itself
     // slice lists (see KArgs): max_batch x FLAT_MAX entries, metadata for up
     // to MAX_SLICES slices per row, one arrival counter per row (zeroed here,
     // reset by every row's finisher)
@@ -4795,6 +4846,9 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     (void)hipGetLastError();
     if (const char *env = getenv("LAL_GPU_LMH_KSPLIT")) c->lmh_ksplit = c->lmh_ksplit && atoi(env) != 0;
     if (const char *env = getenv("LAL_GPU_LIST_ROWS")) c->list_rows = std::min(16, std::max(0, atoi(env)));
+    // measured at [152064, 3584], B = 1: the separate one-round-trip
+    // quantizer before the head is 2.4 us faster than the head's own
+    if (const char *env = getenv("LAL_GPU_HEAD_QX")) c->head_qx = atoi(env) != 0;
     const size_t nl = (size_t)max_batch * FLAT_MAX;
     hipError_t e = hipMalloc((void **)&c->lst_val, nl * sizeof(float));
     if (e == hipSuccess) e = hipMalloc((void **)&c->lst_idx, nl * sizeof(int));
@@ -5338,7 +5392,7 @@ int lal_gpu_lm_head_sample(lal_gpu_ctx *ctx, const float *d_x, int batch, int n,
     const bool cand = batch <= ctx->list_rows && n <= LMX_MAXN && n > 3 * LMM_KC && ctx->lmh_xres != 0 &&
                       !io->allow_bits && !io->bias && ks <= 64 && k_eff <= LAL_GPU_MAX_K;
     // up to QX_ROWS rows the head quantizes the activations itself
-    const bool qx_in = cand && batch <= QX_ROWS && ((uintptr_t)d_x & 15) == 0;
+    const bool qx_in = ctx->head_qx && cand && batch <= QX_ROWS && ((uintptr_t)d_x & 15) == 0;
     if (!qx_in) {
         rc = lal_gpu_quantize_x(ctx, d_x, batch, n, 0, d_xq, d_sx, stream);
         if (rc != LAL_GPU_OK) return rc;

@@ -269,15 +269,23 @@ def test_fused_nan_activation(dev, orc, small_heads):
 
 
 @pytest.mark.parametrize("B", [1, 3])
-def test_fused_quantize_in_head(dev, orc, small_heads, B):
-    """Up to four rows the head quantizes the activations itself: xq, sx and
-    the logits bit-exact with the oracle's quantizer, including a row with an
-    infinity and one with a nan (the AVX2 build's maximum order)."""
-    x = (synth.normal(7600 + B, 0, B * NS).reshape(B, NS) * np.float32(1.5)).astype(np.float32)
-    if B == 3:
-        x[1, 100] = np.float32(np.inf)
-        x[2, NS - 1] = np.float32(np.nan)
-    small_case(dev, orc, small_heads["random"], x, dict(T=0.8, k=5, pen=1.1))
+def test_fused_quantize_in_head(monkeypatch, orc, small_heads, B):
+    """With LAL_GPU_HEAD_QX=1, up to four rows the head quantizes the
+    activations itself: xq, sx and the logits bit-exact with the oracle's
+    quantizer, including a row with an infinity and one with a nan (the AVX2
+    build's maximum order)."""
+    from lal_amd import abi
+    monkeypatch.setenv("LAL_GPU_HEAD_QX", "1")
+    monkeypatch.setenv("LAL_GPU_LIST_ROWS", "16")
+    d = abi.Device(0, max_batch=64, max_vocab=V)
+    try:
+        x = (synth.normal(7600 + B, 0, B * NS).reshape(B, NS) * np.float32(1.5)).astype(np.float32)
+        if B == 3:
+            x[1, 100] = np.float32(np.inf)
+            x[2, NS - 1] = np.float32(np.nan)
+        small_case(d, orc, small_heads["random"], x, dict(T=0.8, k=5, pen=1.1))
+    finally:
+        d.close()
 
 
 def test_fused_bound_check_fails_over(monkeypatch, orc, small_heads):
