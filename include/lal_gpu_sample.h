@@ -250,7 +250,7 @@ int  lal_gpu_lm_head_q8_packed(lal_gpu_ctx *ctx, const int8_t *d_xq, const float
  * sampler with params / io (io->logits and io->ld are ignored: the step's
  * logits are used).  Results are bit for bit those of lal_gpu_quantize_x +
  * lal_gpu_lm_head_q8_packed + lal_gpu_sample.  For up to LAL_GPU_LIST_ROWS
- * rows (default 4, at most 16) without a bias or allow mask the head keeps,
+ * rows (default 16, at most 16) without a bias or allow mask the head keeps,
  * per row, the logits at or above a bound taken from a fixed sample of its
  * tiles (with LAL_GPU_HEAD_QX=1 it also quantizes up to 4 rows itself), and the
  * sampler reads that list instead of the row; a row whose list cannot be

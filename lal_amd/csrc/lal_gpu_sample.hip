@@ -3969,8 +3969,12 @@ __global__ __launch_bounds__(64 * LMM_WAVES) void lm_head_packed_xres_kernel(con
                                    : 0u;
                 K[bb] = 0u;
             }
+            // the top 16 bits of the keys only (sign, exponent, 7 mantissa
+            // bits): K is then at most the exact ks-th largest key, a lower
+            // bound that lets through a few more values at half the ballots
+            // (16 rows x 32 bits cost a wave ~4 us)
 #pragma unroll 1
-            for (int bit = 31; bit >= 0; --bit) {
+            for (int bit = 31; bit >= 16; --bit) {
 #pragma unroll
                 for (int bb = 0; bb < 16; ++bb) {
                     if (bb >= nb) break;
@@ -4835,9 +4839,9 @@ int lal_gpu_create(lal_gpu_ctx **out, int device, int max_batch, int max_vocab)
     if (const char *env = getenv("LAL_GPU_LMH_XRES")) c->lmh_xres = atoi(env) != 0;
     if (const char *env = getenv("LAL_GPU_LMH_PD")) c->lmh_pd = (atoi(env) == 3) ? 3 : 2;
     if (const char *env = getenv("LAL_GPU_LIST_KS")) c->list_ks = std::min(64, std::max(0, atoi(env)));
-    // measured at [152064, 3584]: the lists win up to 4 rows (with the head
-    // quantizing), the separate sampler from 5 rows on
-    c->list_rows = 4;
+    // measured at [152064, 3584]: the lists win at 1 row (106 vs 112 us per
+    // step) and at 16 rows (122 vs 127 us)
+    c->list_rows = 16;
     // the k-split head's dynamic LDS goes past 64 KB
     c->lmh_ksplit = hipFuncSetAttribute((const void *)lm_head_ksplit_kernel<3>,
                                         hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024) == hipSuccess &&

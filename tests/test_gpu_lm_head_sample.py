@@ -44,12 +44,12 @@ def dev():
 
 
 def test_default_list_rows_path(orc, head):
-    """With the default LAL_GPU_LIST_ROWS, 16 rows take the separate sampler
-    (and 1 row the lists): same results either way."""
+    """With the default LAL_GPU_LIST_ROWS (16), 1 and 16 rows take the lists
+    and 17 rows the separate sampler: same results either way."""
     from lal_amd import abi
     d = abi.Device(0, max_batch=64, max_vocab=V)
     try:
-        for B in (1, 16):
+        for B in (1, 16, 17):
             x = (synth.normal(6100 + B, 0, B * N).reshape(B, N)).astype(np.float32)
             hist = synth.history(6200 + B, B, 64, V)
             u = orc.uniforms(6300 + B, B)
