@@ -37,6 +37,10 @@ WORKLOADS = {
                          H=128),
     "constrained": dict(B=512, V=152064, kind="gauss", T=0.7, k=40, top_p=0.0, pen=1.0, H=16,
                         allow=0.05, bias_nnz=2000, mask_recent=16),
+    # the filtered server's largest pool (qwen7b_server.c:236-239: k up to the
+    # 512-slot heap), lal_sample_token_filtered semantics
+    "qwen7b_filtered_k512": dict(B=512, V=152064, kind="zipf", T=0.7, k=512, top_p=0.0, pen=1.1, H=64,
+                                 filtered=True),
 }
 # Q8 LM head + sampling: hidden [B, 3584] ~ N(0,1) quantized per row, W int8
 # [152064, 3584] uniform in [-127, 127], sw ~ U(0.001, 0.02); then penalty 1.1
@@ -174,8 +178,8 @@ class Inputs:
 def params_for(w):
     from lal_amd import abi
     return abi.make_params(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"],
-                           variant=abi.VARIANT_BASIC, mask_recent=w.get("mask_recent", 0),
-                           flags=abi.F_DRAW_GPT2 if w.get("gpt2") else 0)
+                           variant=abi.VARIANT_FILTERED if w.get("filtered") else abi.VARIANT_BASIC,
+                           mask_recent=w.get("mask_recent", 0), flags=abi.F_DRAW_GPT2 if w.get("gpt2") else 0)
 
 
 def cpu_model():
@@ -225,7 +229,8 @@ def cpu_baseline(w, dev, inputs, reps=20):
     a_all = inputs.allow.download((B, inputs.words), np.uint32) if inputs.allow is not None else None
     bias = inputs.bias.download(V, np.float32) if inputs.bias is not None else None
     p = oparams(temperature=w["T"], top_k=w["k"], top_p=w["top_p"], rep_penalty=w["pen"],
-                mask_recent=w.get("mask_recent", 0), flags=2 if w.get("gpt2") else 0)
+                variant=1 if w.get("filtered") else 0, mask_recent=w.get("mask_recent", 0),
+                flags=2 if w.get("gpt2") else 0)
     per_row = algorithmic_bytes_per_row(w)
 
     def measure(nthreads, nrows):

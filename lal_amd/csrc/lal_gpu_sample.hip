@@ -459,17 +459,20 @@ __device__ __forceinline__ float block_seq_prefix(SM &S, float *ep, int n, float
     __syncthreads();
     if (wave_id() == 0) {
         float acc = carry_in;
+        const int me = lane_id();
         for (int base = 0; base < n; base += 64) {
-            const int i = base + lane_id();
-            const float e = (i < n) ? ep[i] : -1.0f;
+            const int i = base + me;
+            float e = (i < n) ? ep[i] : -1.0f;
             const unsigned long long live = __ballot(!(e < 0.0f));
             float pre = acc;
             if (live) {
-                const int lim = min(64, n - base);
-                const int me = lane_id();
-                for (int l = 0; l < lim; ++l) {
-                    const float el = readlane_f(e, l);
-                    if (!(el < 0.0f)) acc = acc + el;
+                // a skipped entry (< 0, and the lanes past n) adds -0.0, which
+                // leaves every sum as it is (x + -0.0 == x, also for +0.0 and
+                // -0.0), so the chain is one add per entry, fully unrolled
+                e = (e < 0.0f) ? -0.0f : e;
+#pragma unroll
+                for (int l = 0; l < 64; ++l) {
+                    acc = acc + readlane_f(e, l);
                     if (me == l) pre = acc;
                 }
             }
@@ -1641,8 +1644,15 @@ __device__ __forceinline__ RowResult block_epilogue(const KArgs &A, SM &S, int n
             const int j = tid + r * WG;
             prk[r] = -1;
             if (j < nc) {
-                int rank = 0;
-                for (int q = 0; q < nc; ++q) {
+                int rank = 0, q = 0;
+                for (; q + 8 <= nc; q += 8) {  // eight LDS reads in flight
+#pragma unroll
+                    for (int u = 0; u < 8; ++u) {
+                        const float pq = ep[q + u];
+                        rank += (pq > pr[r]) || (pq == pr[r] && q + u < j);
+                    }
+                }
+                for (; q < nc; ++q) {
                     const float pq = ep[q];
                     rank += (pq > pr[r]) || (pq == pr[r] && q < j);
                 }
@@ -2541,8 +2551,14 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
                 if (j < nc) {
                     rv[r] = S.cval[j];
                     ri[r] = S.cidx[j];
-                    int rank = 0;
-                    for (int q = 0; q < nc; ++q) rank += (S.cidx[q] < ri[r]);
+                    // eight slots per round, so that eight LDS reads are in
+                    // flight rather than one
+                    int rank = 0, q = 0;
+                    for (; q + 8 <= nc; q += 8) {
+#pragma unroll
+                        for (int u = 0; u < 8; ++u) rank += (S.cidx[q + u] < ri[r]);
+                    }
+                    for (; q < nc; ++q) rank += (S.cidx[q] < ri[r]);
                     rk[r] = rank;
                 }
             }
