@@ -4913,11 +4913,15 @@ void lal_gpu_destroy(lal_gpu_ctx *ctx)
 // (about one per slot: 4 per CU): slices of at least 64 Ki elements, 32 Ki
 // for at most 128 rows, 16 Ki for at most 16 rows; list capacity above k.
 constexpr int TARGET_WGS = 1024;
-static int choose_slices(int batch, int vocab, int k_eff, int flat, int forced)
+// target: the workgroups resident at once (four per CU for the k <= 128
+// instantiation, one for the large-k one, whose LDS takes the CU): more slices
+// than fill it once only add rounds of slice merging (512 rows at k = 512:
+// 363.5 us with 2 slices per row, 275.7 us with 1)
+static int choose_slices(int batch, int vocab, int k_eff, int flat, int forced, int target)
 {
     if (forced >= 1) return std::min(std::min(forced, MAX_SLICES), std::max(1, flat / (k_eff + 1)));
     const int min_len = (batch <= 16) ? 16384 : (batch <= 128) ? 32768 : 65536;
-    int n = (TARGET_WGS + batch - 1) / batch;
+    int n = (target + batch - 1) / batch;
     n = std::min(n, std::max(1, vocab / min_len));
     n = std::min(n, std::max(1, flat / (k_eff + 1)));
     return std::max(1, std::min(n, MAX_SLICES));
@@ -5032,7 +5036,9 @@ static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gp
     const bool small = k_eff <= K_SMALL_MAX;
     const int flat = NWAVE * (small ? CAPW_SMALL : CAPW_LARGE);
     A.batch = batch;
-    A.nslice = (batch <= t.slice_rows) ? choose_slices(batch, vocab, k_eff, flat, t.forced_slices) : 1;
+    A.nslice = (batch <= t.slice_rows)
+                   ? choose_slices(batch, vocab, k_eff, flat, t.forced_slices, small ? TARGET_WGS : TARGET_WGS / 4)
+                   : 1;
     if (t.list) {
         if (A.bias || A.allow) return LAL_GPU_E_INVAL;
         A.nslice = 1;
