@@ -4920,7 +4920,9 @@ constexpr int TARGET_WGS = 1024;
 static int choose_slices(int batch, int vocab, int k_eff, int flat, int forced, int target)
 {
     if (forced >= 1) return std::min(std::min(forced, MAX_SLICES), std::max(1, flat / (k_eff + 1)));
-    const int min_len = (batch <= 16) ? 16384 : (batch <= 128) ? 32768 : 65536;
+    // shortest slice per batch size (measured at 64 x 152064: 6 slices of
+    // 25 K values 1.6 us faster than 4 of 38 K)
+    const int min_len = (batch <= 16) ? 16384 : (batch <= 128) ? 24576 : 65536;
     int n = (target + batch - 1) / batch;
     n = std::min(n, std::max(1, vocab / min_len));
     n = std::min(n, std::max(1, flat / (k_eff + 1)));
