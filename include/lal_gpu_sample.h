@@ -197,7 +197,7 @@ int  lal_gpu_sample(lal_gpu_ctx *ctx, int batch, int vocab,
  * lal_gpu_sample, on the current device; it calls no hipMalloc or hipFree.
  * The candidate lists that the workgroups of a sliced row exchange live in a
  * static per-device scratch array of LAL_GPU_NOALLOC_MAX_ROWS rows (about
- * 4.4 MB, held by each GPU the library runs on until the process ends), set up
+ * 3.3 MB, held by each GPU the library runs on until the process ends), set up
  * on the first call on each device.  Batches of up to that many rows are
  * sliced as lal_gpu_sample slices them; larger batches run one workgroup per
  * row and use no scratch (results never depend on slicing).  A forced slice

@@ -57,7 +57,7 @@ constexpr int EP_ALL = HSLOTS + NWAVE * 256;  // epilogue scratch floats (hval +
 constexpr int RS_CHUNK = NWAVE * 256;         // rescan chunk (lives in the histogram area)
 // per-wave candidate buffer entries: 512 when k <= 128, 2048 up to LAL_GPU_MAX_K
 constexpr int CAPW_SMALL = 512;
-constexpr int CAPW_LARGE = 2048;
+constexpr int CAPW_LARGE = 1536;
 constexpr int K_SMALL_MAX = 128;
 constexpr int MAX_SLICES = 64;                 // slices per row
 constexpr int FLAT_MAX = NWAVE * CAPW_LARGE;   // slice-list entries per row
@@ -4914,9 +4914,10 @@ void lal_gpu_destroy(lal_gpu_ctx *ctx)
 // for at most 128 rows, 16 Ki for at most 16 rows; list capacity above k.
 constexpr int TARGET_WGS = 1024;
 // target: the workgroups resident at once (four per CU for the k <= 128
-// instantiation, one for the large-k one, whose LDS takes the CU): more slices
-// than fill it once only add rounds of slice merging (512 rows at k = 512:
-// 363.5 us with 2 slices per row, 275.7 us with 1)
+// instantiation, two for the large-k one, whose 66 KB of LDS leaves room for
+// two): more slices than fill it once only add rounds of slice merging (512
+// rows at k = 512 with one workgroup per CU: 363.5 us with 2 slices per row,
+// 275.7 us with 1)
 static int choose_slices(int batch, int vocab, int k_eff, int flat, int forced, int target)
 {
     if (forced >= 1) return std::min(std::min(forced, MAX_SLICES), std::max(1, flat / (k_eff + 1)));
@@ -5039,7 +5040,7 @@ static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gp
     const int flat = NWAVE * (small ? CAPW_SMALL : CAPW_LARGE);
     A.batch = batch;
     A.nslice = (batch <= t.slice_rows)
-                   ? choose_slices(batch, vocab, k_eff, flat, t.forced_slices, small ? TARGET_WGS : TARGET_WGS / 4)
+                   ? choose_slices(batch, vocab, k_eff, flat, t.forced_slices, small ? TARGET_WGS : TARGET_WGS / 2)
                    : 1;
     if (t.list) {
         if (A.bias || A.allow) return LAL_GPU_E_INVAL;
@@ -5099,7 +5100,7 @@ static int launch_sample(const ListTarget &t, int batch, int vocab, const lal_gp
 // ---- the sampler without allocation ---------------------------------------
 // Candidate lists and arrival counters of up to LAL_GPU_NOALLOC_MAX_ROWS sliced
 // rows, in one file-scope device array: each GPU the library runs on holds its
-// own copy (about 4.4 MB) until the process ends.  Host code never uses the
+// own copy (about 3.3 MB) until the process ends.  Host code never uses the
 // array's name as an address: its device address comes from
 // hipGetSymbolAddress, once per device, with that device current.
 struct NoallocScratch {
