@@ -2542,6 +2542,85 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
                 }
                 wave_sync();
             }
+        } else if (2 * nc <= NWAVE * CAPW) {
+            int rk_b[PER];
+            // bucket sort by id (ids in the pool are distinct): buckets of
+            // 2^sh ids (at most EP_ALL / 2 of them) are counted and scanned
+            // in the epilogue scratch, the entries dealt into their buckets
+            // at [nc, 2 nc) of the buffers, and each entry's place is its
+            // bucket's start plus the ids below it in the bucket (a few)
+            int sh = 8;
+            while (((V - 1) >> sh) >= EP_ALL / 2) ++sh;
+            const int nbk = ((V - 1) >> sh) + 1;
+            int *bcnt = reinterpret_cast<int *>(S.u.ep);
+            int *boff = bcnt + EP_ALL / 2;
+            for (int i = tid; i < nbk; i += WG) bcnt[i] = 0;
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int j = tid + r * WG;
+                if (j < nc) {
+                    rv[r] = S.cval[j];
+                    ri[r] = S.cidx[j];
+                    atomicAdd(&bcnt[ri[r] >> sh], 1);
+                }
+            }
+            __syncthreads();
+            // exclusive scan of the counts: thread t owns buckets
+            // [t * BPT, t * BPT + BPT)
+            constexpr int BPT = (EP_ALL / 2 + WG - 1) / WG;
+            int lsum = 0;
+#pragma unroll
+            for (int q = 0; q < BPT; ++q) {
+                const int bk = tid * BPT + q;
+                lsum += (bk < nbk) ? bcnt[bk] : 0;
+            }
+            int btot = 0;
+            int run = block_excl_scan(lsum, btot, S.wsum[0]);
+#pragma unroll
+            for (int q = 0; q < BPT; ++q) {
+                const int bk = tid * BPT + q;
+                if (bk < nbk) {
+                    boff[bk] = run;
+                    run += bcnt[bk];
+                }
+            }
+            __syncthreads();
+            float *tv = S.cval + nc;
+            int *ti = S.cidx + nc;
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                if (tid + r * WG < nc) {
+                    const int pos = atomicAdd(&boff[ri[r] >> sh], 1);
+                    tv[pos] = rv[r];
+                    ti[pos] = ri[r];
+                }
+            }
+            __syncthreads();
+            // boff now holds each bucket's end
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                const int pidx = tid + r * WG;
+                if (pidx < nc) {
+                    const int id = ti[pidx];
+                    const int bk = id >> sh;
+                    const int end = boff[bk], start = end - bcnt[bk];
+                    int rank = start;
+                    for (int q = start; q < end; ++q) rank += (ti[q] < id);
+                    rv[r] = tv[pidx];
+                    ri[r] = id;
+                    rk_b[r] = rank;
+                }
+            }
+            __syncthreads();
+#pragma unroll
+            for (int r = 0; r < PER; ++r) {
+                if (tid + r * WG < nc) {
+                    S.cval[rk_b[r]] = rv[r];
+                    S.cidx[rk_b[r]] = ri[r];
+                }
+            }
+            __syncthreads();
         } else {
             int rk[PER];
 #pragma unroll
