@@ -2543,12 +2543,12 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
                 wave_sync();
             }
         } else if (2 * nc <= NWAVE * CAPW) {
-            int rk_b[PER];
             // bucket sort by id (ids in the pool are distinct): buckets of
             // 2^sh ids (at most EP_ALL / 2 of them) are counted and scanned
             // in the epilogue scratch, the entries dealt into their buckets
             // at [nc, 2 nc) of the buffers, and each entry's place is its
             // bucket's start plus the ids below it in the bucket (a few)
+            int rk_b[PER];
             int sh = 8;
             while (((V - 1) >> sh) >= EP_ALL / 2) ++sh;
             const int nbk = ((V - 1) >> sh) + 1;
