@@ -2067,7 +2067,16 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
         for (int i = 0; i < 4; ++i) pm[i] = __ballot(x[i] >= -INFINITY);
         wave_offer<1, CAPW>(bv, bi, hist, R, x, pm, eb, -INFINITY, st, k, &S.tau_key);
     }
-    for (int q0 = qb; q0 < qe; q0 += WITER) {
+    // One wave-iteration: filter the values `c` of quads [q0, q0 + WITER)
+    // (allow / bias words awc, bwc) and issue the loads of the iteration two
+    // ahead into `n2` (words into awn, bwn), every load at a clamped address
+    // (lanes past the share are set to nan where the values are used).  For
+    // the large-k instantiation the three register sets rotate by unrolling
+    // the loop three times, never by copies: a copy of a register still
+    // being loaded waits for that load, which drained every load in flight
+    // once per iteration.
+    auto iter = [&](int q0, const f32x4 (&c)[U4], f32x4 (&n2)[U4], uint32_t awc, uint32_t bwc, uint32_t &awn,
+                    uint32_t &bwn) __attribute__((always_inline)) {
         if (A.prio_rotate) {
             const int itn = (q0 - qb) / WITER;
             if ((itn & 3) == 0) {
@@ -2079,21 +2088,11 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
                 }
             }
         }
-        // two iterations stay in flight while this one is filtered
-        f32x4 nx2[U4];
-        const uint32_t aw2 = HAS_ALLOW ? wload(abits, q0 + 2 * WITER) : 0u;
-        const uint32_t bw2 = HAS_BIAS ? wload(A.bias_bits, q0 + 2 * WITER) : 0u;
-        if (q0 + 3 * WITER <= qe) {
+        awn = HAS_ALLOW ? wload(abits, q0 + 2 * WITER) : 0u;
+        bwn = HAS_BIAS ? wload(A.bias_bits, q0 + 2 * WITER) : 0u;
 #pragma unroll
-            for (int u = 0; u < U4; ++u)
-                nx2[u] = __builtin_nontemporal_load(row4 + q0 + 2 * WITER + u * 64 + lane);
-        } else {
-#pragma unroll
-            for (int u = 0; u < U4; ++u) {
-                const int q = q0 + 2 * WITER + u * 64 + lane;
-                nx2[u] = (q < qe) ? __builtin_nontemporal_load(row4 + q) : f32x4{NAN, NAN, NAN, NAN};
-            }
-        }
+        for (int u = 0; u < U4; ++u)
+            n2[u] = __builtin_nontemporal_load(row4 + min(q0 + 2 * WITER + u * 64 + lane, qe - 1));
         // effective filter: own threshold, or the largest any wave of this
         // row has reached (each is a lower bound of the row's k-th largest);
         // a strict threshold becomes ">=" against the next float up
@@ -2109,23 +2108,24 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
 #pragma unroll
         for (int u = 0; u < U4; ++u) {
             const int rel = ((g.head + 4 * q0) & 31) + 256 * u + 4 * lane;
-            const uint32_t ab = HAS_ALLOW ? window_nibble(aw0, rel, two_words) : 0xFu;
-            const uint32_t bb = HAS_BIAS ? window_nibble(bw0, rel, two_words) : 0u;
+            const uint32_t ab = HAS_ALLOW ? window_nibble(awc, rel, two_words) : 0xFu;
+            const uint32_t bb = HAS_BIAS ? window_nibble(bwc, rel, two_words) : 0u;
 #pragma unroll
-            for (int c = 0; c < 4; ++c) {
-                float v = cur[u][c];
-                if (HAS_BIAS) v = v + (((bb >> c) & 1u) ? bmax : 0.0f);
-                if (HAS_ALLOW && !((ab >> c) & 1u)) v = -INFINITY;
-                x[4 * u + c] = v;
+            for (int cc = 0; cc < 4; ++cc) {
+                float v = c[u][cc];
+                if (HAS_BIAS) v = v + (((bb >> cc) & 1u) ? bmax : 0.0f);
+                if (HAS_ALLOW && !((ab >> cc) & 1u)) v = -INFINITY;
+                x[4 * u + cc] = v;
             }
         }
-        if ((HAS_BIAS || HAS_ALLOW) && q0 + WITER > qe) {
-            // partial last iteration: lanes past the share stay out
+        if (q0 + WITER > qe) {
+            // partial last iteration: lanes past the share (loaded at a
+            // clamped address) stay out
 #pragma unroll
             for (int u = 0; u < U4; ++u)
                 if (q0 + u * 64 + lane >= qe)
 #pragma unroll
-                    for (int c = 0; c < 4; ++c) x[4 * u + c] = NAN;
+                    for (int cc = 0; cc < 4; ++cc) x[4 * u + cc] = NAN;
         }
         // a nan never passes the filter; the row's nans are found here, two
         // values per unordered compare (padding lanes of a partial
@@ -2153,15 +2153,35 @@ __global__ __launch_bounds__(WG) __attribute__((amdgpu_waves_per_eu(LIST ? 1 : 4
             for (int u = 0; u < U4; ++u) eb[u] = g.head + 4 * (q0 + u * 64 + lane);
             wave_offer<U4, CAPW>(bv, bi, hist, R, x, pm, eb, tcmp, st, k, &S.tau_key);
         }
-#pragma unroll
-        for (int u = 0; u < U4; ++u) {
-            cur[u] = nx1[u];
-            nx1[u] = nx2[u];
+    };
+    if constexpr (CAPW > CAPW_SMALL) {
+        f32x4 nx2[U4];
+        uint32_t aw2 = 0u, bw2 = 0u;
+        for (int q0 = qb; q0 < qe; q0 += 3 * WITER) {
+            iter(q0, cur, nx2, aw0, bw0, aw2, bw2);
+            if (q0 + WITER >= qe) break;
+            iter(q0 + WITER, nx1, cur, aw1, bw1, aw0, bw0);
+            if (q0 + 2 * WITER >= qe) break;
+            iter(q0 + 2 * WITER, nx2, nx1, aw2, bw2, aw1, bw1);
         }
-        aw0 = aw1;
-        aw1 = aw2;
-        bw0 = bw1;
-        bw1 = bw2;
+    } else {
+        // within the 128 registers of four workgroups per CU the third set
+        // does not fit: the sets rotate by copies (the loads of the
+        // iteration two ahead fly while this one is filtered)
+        for (int q0 = qb; q0 < qe; q0 += WITER) {
+            f32x4 nx2[U4];
+            uint32_t aw2 = 0u, bw2 = 0u;
+            iter(q0, cur, nx2, aw0, bw0, aw2, bw2);
+#pragma unroll
+            for (int u = 0; u < U4; ++u) {
+                cur[u] = nx1[u];
+                nx1[u] = nx2[u];
+            }
+            aw0 = aw1;
+            aw1 = aw2;
+            bw0 = bw1;
+            bw1 = bw2;
+        }
     }
     }  // stream
     // resolve the entries still holding upper bounds (below the estimate:
